@@ -1,0 +1,135 @@
+/*
+ * sia_attention.h -- C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Each entry point replaces one function of the reference engine's attention
+ * path (Prathmesh234/simple-inference-autoresearch); the reference interface it
+ * stands in for is cited above it as file:line.  The Python package next to
+ * this header binds these symbols with ctypes and keeps the reference's Python
+ * signatures; any other FFI (cgo, JNI, N-API) can bind them the same way.
+ *
+ * Conventions shared by every entry point
+ *  - Tensors are passed as `sia_tensor` descriptors: a device pointer, a dtype,
+ *    the shape and the strides in ELEMENTS (a torch view maps 1:1).  The last
+ *    (head_dim) stride must be 1; other strides may describe any view.
+ *  - Nothing here allocates device memory, synchronises, or keeps per-call
+ *    state: callers own every buffer.  Split-K decode needs a caller-provided
+ *    workspace whose size `sia_decode_workspace_size` reports.
+ *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
+ *    null stream), so every entry point may be captured in a HIP graph.
+ *    `kv_len` is always read on the device.
+ *  - Return value: SIA_OK (0) or a negative `sia_status`; a failing call
+ *    enqueues nothing.  `sia_status_string` names the code and
+ *    `sia_last_error_message` (per thread) says what was wrong.
+ *  - The library targets gfx950 only.
+ */
+#ifndef SIA_ATTENTION_H
+#define SIA_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SIA_ABI_VERSION 1
+#define SIA_MAX_DIMS 5
+
+typedef enum sia_dtype {
+  SIA_F16 = 0,
+  SIA_BF16 = 1,
+  SIA_F32 = 2,
+  SIA_I8 = 3,
+  SIA_I32 = 4,
+  SIA_I64 = 5,
+  SIA_U8 = 6
+} sia_dtype;
+
+typedef enum sia_status {
+  SIA_OK = 0,
+  SIA_ERR_INVALID_ARGUMENT = -1, /* shape / dtype / stride / alignment mismatch */
+  SIA_ERR_UNSUPPORTED = -2,      /* valid but not implemented (e.g. head_dim 48) */
+  SIA_ERR_WORKSPACE = -3,        /* workspace missing or too small */
+  SIA_ERR_LAUNCH = -4,           /* the HIP runtime refused the launch */
+  SIA_ERR_DEVICE = -5            /* no device / not a gfx950 device */
+} sia_status;
+
+typedef struct sia_tensor {
+  void* data;                     /* device pointer */
+  int32_t dtype;                  /* sia_dtype */
+  int32_t ndim;                   /* 0..SIA_MAX_DIMS */
+  int64_t shape[SIA_MAX_DIMS];
+  int64_t stride[SIA_MAX_DIMS];   /* in elements */
+} sia_tensor;
+
+/* Optional tuning knobs for the decode family; pass NULL for the defaults. */
+typedef struct sia_decode_options {
+  int32_t tiles_per_split;  /* 0 = automatic; else force this many 16-token tiles per split-K item */
+  int32_t reserved[7];      /* must be zero */
+} sia_decode_options;
+
+int sia_abi_version(void);
+const char* sia_status_string(int status);
+const char* sia_last_error_message(void);
+
+/* Bytes of workspace the decode entry points need for split-K partials and
+ * their device-side plan, for this batch/head geometry on the current device. */
+int sia_decode_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads,
+                              int64_t head_dim, size_t* bytes);
+
+/* Replaces attention_flash_decode (kernels/flash_decode_kernel.py:119-160).
+ * q (B,Hq,1,D) f16|bf16; k,v (B,Hkv,S,D) same dtype as q (views into the cache);
+ * kv_len int32 (1,)|()|(B,) on device; out (B,1,Hq,D) dtype of q. */
+int sia_attention_flash_decode(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v,
+                               const sia_tensor* kv_len, float sm_scale, const sia_tensor* out,
+                               void* workspace, size_t workspace_bytes,
+                               const sia_decode_options* opts, void* stream);
+
+/* Replaces attention_flash_decode_int8 (kernels/flash_decode_int8_kernel.py:121-167).
+ * k_int8,v_int8 (B,Hkv,S,D) int8; k_scale,v_scale (B,Hkv,S) f32|f16. */
+int sia_attention_flash_decode_int8(const sia_tensor* q, const sia_tensor* k_int8,
+                                    const sia_tensor* v_int8, const sia_tensor* k_scale,
+                                    const sia_tensor* v_scale, const sia_tensor* kv_len,
+                                    float sm_scale, const sia_tensor* out, void* workspace,
+                                    size_t workspace_bytes, const sia_decode_options* opts,
+                                    void* stream);
+
+/* Replaces gqa_int8_flash_decode (kernels/paged_flash_decode_int8_gqa_kernel.py:100-124).
+ * Same arguments as sia_attention_flash_decode_int8; every kernel of this
+ * library already reads each KV head once per GQA group. */
+int sia_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_int8,
+                              const sia_tensor* v_int8, const sia_tensor* k_scale,
+                              const sia_tensor* v_scale, const sia_tensor* kv_len,
+                              float sm_scale, const sia_tensor* out, void* workspace,
+                              size_t workspace_bytes, const sia_decode_options* opts,
+                              void* stream);
+
+/* Replaces paged_attention_flash_decode (kernels/paged_flash_decode_kernel.py:107-152).
+ * k_pool,v_pool (num_pages,Hkv,page_size,D) f16|bf16; block_table (B,max_blocks)
+ * int32; page_size a multiple of 16 (16 * 2^k). */
+int sia_paged_attention_flash_decode(const sia_tensor* q, const sia_tensor* k_pool,
+                                     const sia_tensor* v_pool, const sia_tensor* block_table,
+                                     const sia_tensor* kv_len, int32_t page_size, float sm_scale,
+                                     const sia_tensor* out, void* workspace,
+                                     size_t workspace_bytes, const sia_decode_options* opts,
+                                     void* stream);
+
+/* New composition for BASELINE configs 3 and 5 (paged pool + int8 + GQA group
+ * per KV head); argument meaning follows paged_attention_flash_decode
+ * (kernels/paged_flash_decode_kernel.py:107) and gqa_int8_flash_decode
+ * (kernels/paged_flash_decode_int8_gqa_kernel.py:100).
+ * k_pool,v_pool (num_pages,Hkv,page_size,D) int8; k_scale_pool,v_scale_pool
+ * (num_pages,Hkv,page_size) f32|f16. */
+int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_pool,
+                                    const sia_tensor* v_pool, const sia_tensor* k_scale_pool,
+                                    const sia_tensor* v_scale_pool,
+                                    const sia_tensor* block_table, const sia_tensor* kv_len,
+                                    int32_t page_size, float sm_scale, const sia_tensor* out,
+                                    void* workspace, size_t workspace_bytes,
+                                    const sia_decode_options* opts, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SIA_ATTENTION_H */

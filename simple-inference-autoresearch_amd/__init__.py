@@ -1,0 +1,41 @@
+"""MI355X-native (gfx950) attention hot path for simple-inference-autoresearch.
+
+Drop-in replacements for the reference engine's attention functions, backed by
+hand-written HIP kernels in ``libsia_attention.so`` (C ABI:
+``include/sia_attention.h``).  The package directory name contains hyphens, so
+import it with ``importlib.import_module("simple-inference-autoresearch_amd")``.
+
+Importing the package never needs a GPU; calling a kernel does, and raises
+``LibraryMissing`` when the HIP library is not built (there is no CPU path).
+"""
+
+from __future__ import annotations
+
+import torch  # noqa: F401  (load torch's HIP runtime before the library)
+
+from ._lib import LibraryMissing, SiaError, exported_symbols, library_path, load_library, require_library
+from .decode import (
+    attention_flash_decode,
+    attention_flash_decode_int8,
+    decode_options,
+    decode_workspace_size,
+    gqa_int8_flash_decode,
+    paged_attention_flash_decode,
+    paged_gqa_int8_flash_decode,
+)
+
+__all__ = [
+    "LibraryMissing",
+    "SiaError",
+    "attention_flash_decode",
+    "attention_flash_decode_int8",
+    "decode_options",
+    "decode_workspace_size",
+    "exported_symbols",
+    "gqa_int8_flash_decode",
+    "library_path",
+    "load_library",
+    "paged_attention_flash_decode",
+    "paged_gqa_int8_flash_decode",
+    "require_library",
+]

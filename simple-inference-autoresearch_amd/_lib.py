@@ -1,0 +1,171 @@
+"""ctypes binding of ``libsia_attention.so`` (the gfx950 C ABI in include/sia_attention.h).
+
+The library is loaded lazily, after ``import torch`` so that it shares torch's
+HIP runtime (both resolve ``libamdhip64.so.7``).  There is no fallback: when the
+library is missing every kernel call raises ``LibraryMissing``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libsia_attention.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+SIA_MAX_DIMS = 5
+SIA_F16, SIA_BF16, SIA_F32, SIA_I8, SIA_I32, SIA_I64, SIA_U8 = range(7)
+
+SIA_OK = 0
+SIA_ERR_INVALID_ARGUMENT = -1
+SIA_ERR_UNSUPPORTED = -2
+SIA_ERR_WORKSPACE = -3
+SIA_ERR_LAUNCH = -4
+SIA_ERR_DEVICE = -5
+
+_DTYPE_CODES = {
+    torch.float16: SIA_F16,
+    torch.bfloat16: SIA_BF16,
+    torch.float32: SIA_F32,
+    torch.int8: SIA_I8,
+    torch.int32: SIA_I32,
+    torch.int64: SIA_I64,
+    torch.uint8: SIA_U8,
+}
+
+
+class LibraryMissing(RuntimeError):
+    """The HIP library is not built or cannot be loaded (no CPU fallback exists)."""
+
+
+class SiaError(RuntimeError):
+    """A launch or device failure reported by the library."""
+
+
+class SiaTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("dtype", ctypes.c_int32),
+        ("ndim", ctypes.c_int32),
+        ("shape", ctypes.c_int64 * SIA_MAX_DIMS),
+        ("stride", ctypes.c_int64 * SIA_MAX_DIMS),
+    ]
+
+
+class DecodeOptions(ctypes.Structure):
+    _fields_ = [("tiles_per_split", ctypes.c_int32), ("reserved", ctypes.c_int32 * 7)]
+
+
+_P = ctypes.POINTER(SiaTensor)
+_VP = ctypes.c_void_p
+_SZ = ctypes.c_size_t
+_F = ctypes.c_float
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+
+# name -> argtypes (restype is int for every entry point)
+_SIGNATURES = {
+    "sia_abi_version": [],
+    "sia_status_string": [ctypes.c_int],
+    "sia_last_error_message": [],
+    "sia_decode_workspace_size": [_I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)],
+    "sia_attention_flash_decode": [_P, _P, _P, _P, _F, _P, _VP, _SZ, ctypes.POINTER(DecodeOptions), _VP],
+    "sia_attention_flash_decode_int8": [_P, _P, _P, _P, _P, _P, _F, _P, _VP, _SZ,
+                                        ctypes.POINTER(DecodeOptions), _VP],
+    "sia_gqa_int8_flash_decode": [_P, _P, _P, _P, _P, _P, _F, _P, _VP, _SZ,
+                                  ctypes.POINTER(DecodeOptions), _VP],
+    "sia_paged_attention_flash_decode": [_P, _P, _P, _P, _P, _I32, _F, _P, _VP, _SZ,
+                                         ctypes.POINTER(DecodeOptions), _VP],
+    "sia_paged_gqa_int8_flash_decode": [_P, _P, _P, _P, _P, _P, _P, _I32, _F, _P, _VP, _SZ,
+                                        ctypes.POINTER(DecodeOptions), _VP],
+}
+_STRING_RESULT = {"sia_status_string", "sia_last_error_message"}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def exported_symbols():
+    """Names of the C entry points this binding expects the library to export."""
+    return sorted(_SIGNATURES)
+
+
+def load_library():
+    """Load (once) and return the ctypes handle; raise LibraryMissing if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(
+                f"{LIB_NAME} is not built (expected at {LIB_PATH}); run __graft_entry__.build() "
+                "or python simple-inference-autoresearch_amd/csrc/build.py")
+        try:
+            h = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+        except OSError as exc:  # pragma: no cover - depends on the host
+            raise LibraryMissing(f"cannot load {LIB_PATH}: {exc}") from exc
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_char_p if name in _STRING_RESULT else ctypes.c_int
+        if h.sia_abi_version() != 1:
+            raise LibraryMissing("libsia_attention.so ABI version mismatch; rebuild it")
+        _lib = h
+        return _lib
+
+
+def require_library():
+    """Raise unless the library is loaded and a GPU is visible to torch."""
+    h = load_library()
+    if not torch.cuda.is_available():
+        raise LibraryMissing("no GPU is visible; the attention kernels run on MI355X (gfx950) only")
+    return h
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dt]
+    except KeyError:
+        raise ValueError(f"dtype {dt} is not supported by the attention kernels") from None
+
+
+def desc(t: torch.Tensor) -> SiaTensor:
+    """Describe a device tensor (pointer, dtype, shape, element strides)."""
+    if t.dim() > SIA_MAX_DIMS:
+        raise ValueError(f"tensor with {t.dim()} dims; at most {SIA_MAX_DIMS} supported")
+    d = SiaTensor()
+    d.data = t.data_ptr()
+    d.dtype = dtype_code(t.dtype)
+    d.ndim = t.dim()
+    for i, (n, s) in enumerate(zip(t.shape, t.stride())):
+        d.shape[i] = n
+        d.stride[i] = s
+    return d
+
+
+def check(rc: int) -> None:
+    """Map a library status to the exception the reference's wrappers would raise."""
+    if rc == SIA_OK:
+        return
+    h = load_library()
+    msg = (h.sia_last_error_message() or b"").decode(errors="replace")
+    kind = (h.sia_status_string(rc) or b"").decode(errors="replace")
+    text = f"{kind}: {msg}" if msg else kind
+    if rc == SIA_ERR_INVALID_ARGUMENT:
+        raise ValueError(text)
+    if rc == SIA_ERR_UNSUPPORTED:
+        raise NotImplementedError(text)
+    raise SiaError(text)
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,302 @@
+// extern "C" decode entry points: validation, workspace layout, dispatch.
+#include <math.h>
+#include <string.h>
+
+#include "decode_launch.hpp"
+#include "host_util.hpp"
+
+namespace sia {
+const char* last_message();
+}
+
+using namespace sia;
+
+namespace {
+
+constexpr int kPlanHeader = 4;
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+struct Geometry {
+  int B, Hq, Hkv, D, G, HG, U, G16;
+};
+
+size_t plan_bytes(int B) { return (size_t)round_up((int64_t)(kPlanHeader + B + 1) * 4, 256); }
+size_t item_bytes(const Geometry& g) { return (size_t)g.G16 * (g.D + 2) * 4; }
+
+// Items the workspace must be able to hold: at most ~4 per persistent
+// work-group plus one per (sequence, unit) (see plan_items in decode_kernel.hpp).
+int64_t wanted_items(const Geometry& g) {
+  const int cus = device_info().cus > 0 ? device_info().cus : 256;
+  return 4LL * cus * 8 + (int64_t)g.B * g.U + 64;
+}
+
+int geometry(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, Geometry& g) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || D <= 0)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "batch, heads and head_dim must be positive");
+  if (Hq % Hkv != 0)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "num_q_heads (%lld) must be a multiple of num_kv_heads (%lld)",
+                (long long)Hq, (long long)Hkv);
+  if (B > 16384) return fail(SIA_ERR_UNSUPPORTED, "batch %lld exceeds 16384", (long long)B);
+  g.B = (int)B; g.Hq = (int)Hq; g.Hkv = (int)Hkv; g.D = (int)D;
+  g.G = (int)(Hq / Hkv);
+  g.HG = (g.G + 15) / 16;
+  g.U = g.Hkv * g.HG;
+  g.G16 = g.G < 16 ? g.G : 16;
+  return SIA_OK;
+}
+
+int check_tensor(const sia_tensor* t, const char* name, int ndim) {
+  if (t == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+  if (t->data == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "%s has no data pointer", name);
+  if (t->ndim != ndim)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "%s must have %d dims, got %d", name, ndim, t->ndim);
+  return SIA_OK;
+}
+
+// Common checks of q/out/kv_len and fill of the q/out/len fields.
+int prepare_common(const sia_tensor* q, const sia_tensor* kv_len, const sia_tensor* out, int Hkv,
+                   float sm_scale, Geometry& g, DecodeLaunch& L) {
+  int rc;
+  if ((rc = check_tensor(q, "q", 4))) return rc;
+  if ((rc = check_tensor(out, "out", 4))) return rc;
+  if (kv_len == nullptr || kv_len->data == nullptr)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "kv_len is missing");
+  if (q->dtype != SIA_F16 && q->dtype != SIA_BF16)
+    return fail(SIA_ERR_UNSUPPORTED, "q dtype %s: expected float16 or bfloat16", dtype_name(q->dtype));
+  if (q->shape[2] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "decode kernel expects a single query position");
+  if ((rc = geometry(q->shape[0], q->shape[1], Hkv, q->shape[3], g))) return rc;
+  if (g.D != 64 && g.D != 128 && g.D != 256)
+    return fail(SIA_ERR_UNSUPPORTED, "unsupported head_dim %d (this build supports 64, 128, 256)", g.D);
+  if (q->stride[3] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "q must be contiguous along head_dim");
+  if (!aligned16(q->data) || bstride(q, 0) % 16 || bstride(q, 1) % 16)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "q rows must be 16-byte aligned");
+  if (out->dtype != q->dtype) return fail(SIA_ERR_INVALID_ARGUMENT, "out dtype must equal q dtype");
+  if (out->shape[0] != g.B || out->shape[1] != 1 || out->shape[2] != g.Hq || out->shape[3] != g.D)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "out must be (B, 1, Hq, D)");
+  if (out->stride[3] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "out must be contiguous along head_dim");
+  if (kv_len->dtype != SIA_I32) return fail(SIA_ERR_INVALID_ARGUMENT, "kv_len must be int32");
+  int64_t n = 1;
+  for (int i = 0; i < kv_len->ndim; ++i) n *= kv_len->shape[i];
+  if (kv_len->ndim > 1 || (n != 1 && n != g.B))
+    return fail(SIA_ERR_INVALID_ARGUMENT, "kv_len must be a scalar, (1,) or (B,) tensor");
+  if (n == g.B && g.B > 1 && kv_len->ndim == 1 && kv_len->stride[0] != 1)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "kv_len must be contiguous");
+  if (!(sm_scale > 0.0f) || !isfinite(sm_scale))
+    return fail(SIA_ERR_INVALID_ARGUMENT, "sm_scale must be a positive finite number");
+  const DeviceInfo& dev = device_info();
+  if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
+  if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
+
+  DecodeArgs& a = L.a;
+  memset(&a, 0, sizeof(a));
+  a.q = (const char*)q->data; a.q_sb = bstride(q, 0); a.q_sh = bstride(q, 1);
+  a.out = (char*)out->data; a.o_sb = bstride(out, 0); a.o_sh = bstride(out, 2);
+  a.kv_len = (const int32_t*)kv_len->data;
+  a.kv_per_seq = (n == g.B && g.B > 1) ? 1 : 0;
+  a.B = g.B; a.Hq = g.Hq; a.Hkv = g.Hkv; a.G = g.G; a.HG = g.HG; a.U = g.U; a.G16 = g.G16;
+  a.qk_scale = sm_scale * 1.4426950408889634f;
+  L.D = g.D;
+  L.q_dtype = q->dtype;
+  return SIA_OK;
+}
+
+// K/V (and scale) layout checks.  Contiguous: (B', Hkv, S, D) with B' >= B.
+// Paged: (num_pages, Hkv, page_size, D).
+int prepare_kv(const sia_tensor* k, const sia_tensor* v, const Geometry& g, bool paged, int page_size,
+               DecodeLaunch& L) {
+  int rc;
+  if ((rc = check_tensor(k, "k", 4))) return rc;
+  if ((rc = check_tensor(v, "v", 4))) return rc;
+  if (k->dtype != v->dtype) return fail(SIA_ERR_INVALID_ARGUMENT, "k and v dtypes differ");
+  for (int d = 0; d < 4; ++d)
+    if (k->shape[d] != v->shape[d]) return fail(SIA_ERR_INVALID_ARGUMENT, "k and v shapes differ");
+  if (k->shape[1] != g.Hkv || k->shape[3] != g.D)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be (*, Hkv=%d, *, D=%d)", g.Hkv, g.D);
+  if (k->stride[3] != 1 || v->stride[3] != 1)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be contiguous along head_dim");
+  if (!aligned16(k->data) || !aligned16(v->data))
+    return fail(SIA_ERR_INVALID_ARGUMENT, "k/v base pointers must be 16-byte aligned");
+  for (int d = 0; d < 3; ++d)
+    if (bstride(k, d) % 16 || bstride(v, d) % 16)
+      return fail(SIA_ERR_INVALID_ARGUMENT, "k/v strides must be multiples of 16 bytes");
+  DecodeArgs& a = L.a;
+  a.k = (const char*)k->data; a.k_s0 = bstride(k, 0); a.k_sh = bstride(k, 1); a.k_sn = bstride(k, 2);
+  a.v = (const char*)v->data; a.v_s0 = bstride(v, 0); a.v_sh = bstride(v, 1); a.v_sn = bstride(v, 2);
+  if (paged) {
+    if (k->shape[2] != page_size)
+      return fail(SIA_ERR_INVALID_ARGUMENT, "k_pool page dim %lld != page_size %d", (long long)k->shape[2], page_size);
+    if (page_size < 16 || page_size % 16 || ((page_size / 16) & (page_size / 16 - 1)))
+      return fail(SIA_ERR_UNSUPPORTED, "page_size %d: this build supports 16 * 2^k", page_size);
+    int lg = 0;
+    while ((16 << lg) < page_size) ++lg;
+    a.lg_tiles_per_page = lg;
+    a.num_pages = k->shape[0];
+  } else {
+    if (k->shape[0] < g.B) return fail(SIA_ERR_INVALID_ARGUMENT, "k/v batch dim smaller than q's");
+    if (k->shape[2] > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "cache length too large");
+    a.cap_tokens = (int)k->shape[2];
+  }
+  return SIA_OK;
+}
+
+int prepare_scales(const sia_tensor* ks, const sia_tensor* vs, const sia_tensor* k, DecodeLaunch& L) {
+  int rc;
+  if ((rc = check_tensor(ks, "k_scale", 3))) return rc;
+  if ((rc = check_tensor(vs, "v_scale", 3))) return rc;
+  if (ks->dtype != vs->dtype || (ks->dtype != SIA_F32 && ks->dtype != SIA_F16))
+    return fail(SIA_ERR_UNSUPPORTED, "k_scale/v_scale must both be float32 or float16");
+  for (int d = 0; d < 3; ++d)
+    if (ks->shape[d] != k->shape[d] || vs->shape[d] != k->shape[d])
+      return fail(SIA_ERR_INVALID_ARGUMENT, "scale shape must be the K/V shape without head_dim");
+  DecodeArgs& a = L.a;
+  a.ks = (const char*)ks->data; a.ks_s0 = bstride(ks, 0); a.ks_sh = bstride(ks, 1); a.ks_sn = bstride(ks, 2);
+  a.vs = (const char*)vs->data; a.vs_s0 = bstride(vs, 0); a.vs_sh = bstride(vs, 1); a.vs_sn = bstride(vs, 2);
+  L.scale_dtype = ks->dtype;
+  a.scale_vec = ks->dtype == SIA_F32 && ks->stride[2] == 1 && vs->stride[2] == 1 && aligned16(ks->data) &&
+                aligned16(vs->data) && bstride(ks, 0) % 16 == 0 && bstride(ks, 1) % 16 == 0 &&
+                bstride(vs, 0) % 16 == 0 && bstride(vs, 1) % 16 == 0;
+  return SIA_OK;
+}
+
+int prepare_table(const sia_tensor* bt, const Geometry& g, int page_size, DecodeLaunch& L) {
+  int rc;
+  if ((rc = check_tensor(bt, "block_table", 2))) return rc;
+  if (bt->dtype != SIA_I32) return fail(SIA_ERR_INVALID_ARGUMENT, "block_table must be int32");
+  if (bt->shape[0] < g.B) return fail(SIA_ERR_INVALID_ARGUMENT, "block_table has fewer rows than the batch");
+  const int64_t cap = bt->shape[1] * (int64_t)page_size;
+  if (cap > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "block table capacity too large");
+  DecodeArgs& a = L.a;
+  a.bt = (const int32_t*)bt->data; a.bt_sb = bt->stride[0]; a.bt_sl = bt->stride[1];
+  a.cap_tokens = (int)cap;
+  return SIA_OK;
+}
+
+int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decode_options* opts, DecodeLaunch& L) {
+  if (opts != nullptr) {
+    for (int i = 0; i < 7; ++i)
+      if (opts->reserved[i] != 0) return fail(SIA_ERR_INVALID_ARGUMENT, "sia_decode_options.reserved must be zero");
+    if (opts->tiles_per_split < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "tiles_per_split must be >= 0");
+  }
+  const size_t pb = plan_bytes(g.B);
+  const size_t ib = item_bytes(g);
+  if (ws == nullptr || bytes < pb + ib * (size_t)g.B * g.U || !aligned16(ws))
+    return fail(SIA_ERR_WORKSPACE, "decode workspace missing, misaligned or smaller than %zu bytes",
+                pb + ib * (size_t)g.B * g.U);
+  int64_t items = (int64_t)((bytes - pb) / ib);
+  if (items > 0x7fffffff) items = 0x7fffffff;
+  DecodeArgs& a = L.a;
+  a.ws_plan = (int32_t*)ws;
+  a.max_items = (int32_t)items;
+  a.ws_ml = (float*)((char*)ws + pb);
+  a.ws_acc = a.ws_ml + (size_t)items * g.G16 * 2;
+  a.tps_force = opts ? opts->tiles_per_split : 0;
+  return SIA_OK;
+}
+
+int dispatch(DecodeLaunch& L, int kv_dtype) {
+  switch (kv_dtype) {
+    case SIA_F16: return launch_decode_f16(L);
+    case SIA_BF16: return launch_decode_bf16(L);
+    case SIA_I8: return launch_decode_i8(L);
+    default: return fail(SIA_ERR_UNSUPPORTED, "k/v dtype %s not supported", dtype_name(kv_dtype));
+  }
+}
+
+int decode_any(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, const sia_tensor* ks,
+               const sia_tensor* vs, const sia_tensor* bt, const sia_tensor* kv_len, int page_size,
+               float sm_scale, const sia_tensor* out, void* ws, size_t ws_bytes,
+               const sia_decode_options* opts, void* stream, bool want_int8) {
+  DecodeLaunch L;
+  Geometry g;
+  int rc;
+  if (k == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "k is NULL");
+  if ((rc = prepare_common(q, kv_len, out, (int)k->shape[1], sm_scale, g, L))) return rc;
+  if ((rc = prepare_kv(k, v, g, bt != nullptr, page_size, L))) return rc;
+  if (want_int8) {
+    if (k->dtype != SIA_I8) return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be int8 for the int8 entry points");
+    if ((rc = prepare_scales(ks, vs, k, L))) return rc;
+  } else if (k->dtype != SIA_F16 && k->dtype != SIA_BF16) {
+    return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be float16 or bfloat16 (use the int8 entry points for int8)");
+  }
+  if (bt != nullptr && (rc = prepare_table(bt, g, page_size, L))) return rc;
+  if ((rc = prepare_workspace(ws, ws_bytes, g, opts, L))) return rc;
+  L.stream = (hipStream_t)stream;
+  return dispatch(L, k->dtype);
+}
+
+}  // namespace
+
+extern "C" {
+
+int sia_abi_version(void) { return SIA_ABI_VERSION; }
+
+const char* sia_status_string(int status) {
+  switch (status) {
+    case SIA_OK: return "ok";
+    case SIA_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case SIA_ERR_UNSUPPORTED: return "unsupported";
+    case SIA_ERR_WORKSPACE: return "workspace too small";
+    case SIA_ERR_LAUNCH: return "launch failed";
+    case SIA_ERR_DEVICE: return "device error";
+    default: return "unknown status";
+  }
+}
+
+const char* sia_last_error_message(void) { return sia::last_message(); }
+
+int sia_decode_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv_heads, int64_t head_dim,
+                              size_t* bytes) {
+  if (bytes == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  Geometry g;
+  int rc = geometry(batch, num_q_heads, num_kv_heads, head_dim, g);
+  if (rc) return rc;
+  *bytes = plan_bytes(g.B) + item_bytes(g) * (size_t)wanted_items(g);
+  return SIA_OK;
+}
+
+int sia_attention_flash_decode(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v,
+                               const sia_tensor* kv_len, float sm_scale, const sia_tensor* out,
+                               void* workspace, size_t workspace_bytes, const sia_decode_options* opts,
+                               void* stream) {
+  return decode_any(q, k, v, nullptr, nullptr, nullptr, kv_len, 0, sm_scale, out, workspace,
+                    workspace_bytes, opts, stream, false);
+}
+
+int sia_attention_flash_decode_int8(const sia_tensor* q, const sia_tensor* k_int8, const sia_tensor* v_int8,
+                                    const sia_tensor* k_scale, const sia_tensor* v_scale,
+                                    const sia_tensor* kv_len, float sm_scale, const sia_tensor* out,
+                                    void* workspace, size_t workspace_bytes, const sia_decode_options* opts,
+                                    void* stream) {
+  return decode_any(q, k_int8, v_int8, k_scale, v_scale, nullptr, kv_len, 0, sm_scale, out, workspace,
+                    workspace_bytes, opts, stream, true);
+}
+
+int sia_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_int8, const sia_tensor* v_int8,
+                              const sia_tensor* k_scale, const sia_tensor* v_scale, const sia_tensor* kv_len,
+                              float sm_scale, const sia_tensor* out, void* workspace, size_t workspace_bytes,
+                              const sia_decode_options* opts, void* stream) {
+  return decode_any(q, k_int8, v_int8, k_scale, v_scale, nullptr, kv_len, 0, sm_scale, out, workspace,
+                    workspace_bytes, opts, stream, true);
+}
+
+int sia_paged_attention_flash_decode(const sia_tensor* q, const sia_tensor* k_pool, const sia_tensor* v_pool,
+                                     const sia_tensor* block_table, const sia_tensor* kv_len, int32_t page_size,
+                                     float sm_scale, const sia_tensor* out, void* workspace,
+                                     size_t workspace_bytes, const sia_decode_options* opts, void* stream) {
+  if (block_table == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "block_table is NULL");
+  return decode_any(q, k_pool, v_pool, nullptr, nullptr, block_table, kv_len, page_size, sm_scale, out,
+                    workspace, workspace_bytes, opts, stream, false);
+}
+
+int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_pool, const sia_tensor* v_pool,
+                                    const sia_tensor* k_scale_pool, const sia_tensor* v_scale_pool,
+                                    const sia_tensor* block_table, const sia_tensor* kv_len, int32_t page_size,
+                                    float sm_scale, const sia_tensor* out, void* workspace,
+                                    size_t workspace_bytes, const sia_decode_options* opts, void* stream) {
+  if (block_table == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "block_table is NULL");
+  return decode_any(q, k_pool, v_pool, k_scale_pool, v_scale_pool, block_table, kv_len, page_size, sm_scale,
+                    out, workspace, workspace_bytes, opts, stream, true);
+}
+
+}  // extern "C"

@@ -1,0 +1,66 @@
+// Host-side launch of the decode kernels (one instantiation unit per K/V dtype).
+#pragma once
+
+#include <type_traits>
+
+#include "decode_kernel.hpp"
+#include "host_util.hpp"
+
+namespace sia {
+
+constexpr int kDecodeWaves = 4;   // waves per work-group
+
+struct DecodeLaunch {
+  DecodeArgs a;
+  int D;
+  int q_dtype;       // SIA_F16 / SIA_BF16 (also the output dtype)
+  int scale_dtype;   // SIA_F32 / SIA_F16 (int8 only)
+  hipStream_t stream;
+};
+
+inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
+  return (size_t)NW * G16 * D * 4 + (size_t)2 * NW * G16 * 4 + (size_t)(2 * NW + 2) * 4 +
+         (size_t)(B + 1) * 4;
+}
+
+template <int D, class KV, class QT, class ST>
+int launch_decode_typed(DecodeLaunch& L) {
+  constexpr int NW = kDecodeWaves;
+  auto kmain = decode_main<D, KV, QT, ST, NW>;
+  const size_t lds = decode_lds_bytes(D, L.a.G16, L.a.B, NW);
+  int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
+  if (occ <= 0) return fail(SIA_ERR_LAUNCH, "decode kernel does not fit on a CU (LDS %zu B)", lds);
+  const int slots = device_info().cus * occ;
+  hipLaunchKernelGGL(kmain, dim3(slots), dim3(NW * 64), lds, L.stream, L.a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode launch: %s", hipGetErrorString(e));
+  const int rows = L.a.B * L.a.Hq;
+  hipLaunchKernelGGL((decode_reduce<D, QT>), dim3((rows + 3) / 4), dim3(256), 0, L.stream, L.a);
+  e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode reduce launch: %s", hipGetErrorString(e));
+  return SIA_OK;
+}
+
+template <class KV, class QT, class ST>
+int launch_decode_d(DecodeLaunch& L) {
+  switch (L.D) {
+    case 64: return launch_decode_typed<64, KV, QT, ST>(L);
+    case 128: return launch_decode_typed<128, KV, QT, ST>(L);
+    case 256: return launch_decode_typed<256, KV, QT, ST>(L);
+    default: return fail(SIA_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", L.D);
+  }
+}
+
+template <class KV, class ST>
+int launch_decode_q(DecodeLaunch& L) {
+  if (L.q_dtype == SIA_F16) return launch_decode_d<KV, F16, ST>(L);
+  if (L.q_dtype == SIA_BF16) return launch_decode_d<KV, BF16, ST>(L);
+  return fail(SIA_ERR_UNSUPPORTED, "query dtype must be float16 or bfloat16");
+}
+
+// Entry points implemented by decode_f16.hip / decode_bf16.hip / decode_i8.hip.
+int launch_decode_f16(DecodeLaunch& L);
+int launch_decode_bf16(DecodeLaunch& L);
+int launch_decode_i8(DecodeLaunch& L);
+
+}  // namespace sia

@@ -1,0 +1,157 @@
+// Shared device/host helpers for the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "sia_attention.h"
+
+namespace sia {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// Element-type tags.  `bytes` is the storage size; the MFMA input type of a
+// 16-bit tag is itself, int8 K/V feed the f16 MFMA after an exact conversion.
+struct F16 { static constexpr int bytes = 2; static constexpr int code = SIA_F16; };
+struct BF16 { static constexpr int bytes = 2; static constexpr int code = SIA_BF16; };
+struct I8 { static constexpr int bytes = 1; static constexpr int code = SIA_I8; };
+struct F32 { static constexpr int bytes = 4; static constexpr int code = SIA_F32; };
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float to_f32(F16, uint16_t bits) {
+  return (float)__builtin_bit_cast(_Float16, bits);
+}
+__device__ __forceinline__ float to_f32(BF16, uint16_t bits) {
+  return __builtin_bit_cast(float, (uint32_t)bits << 16);
+}
+
+// Round-to-nearest-even conversions of two floats into one packed 16-bit pair
+// (low half = a).
+__device__ __forceinline__ uint32_t pack2(F16, float a, float b) {
+  f16x2 h = {(_Float16)a, (_Float16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ uint32_t pack2(BF16, float a, float b) {
+  bf16x2 h = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, h);
+}
+__device__ __forceinline__ float lo_f32(F16, uint32_t w) { return to_f32(F16{}, (uint16_t)(w & 0xffffu)); }
+__device__ __forceinline__ float hi_f32(F16, uint32_t w) { return to_f32(F16{}, (uint16_t)(w >> 16)); }
+__device__ __forceinline__ float lo_f32(BF16, uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float hi_f32(BF16, uint32_t w) { return __builtin_bit_cast(float, w & 0xffff0000u); }
+
+__device__ __forceinline__ void store_out(F16, char* p, float x) {
+  *(_Float16*)p = (_Float16)x;
+}
+__device__ __forceinline__ void store_out(BF16, char* p, float x) {
+  *(__bf16*)p = (__bf16)x;
+}
+__device__ __forceinline__ void store_out(F32, char* p, float x) { *(float*)p = x; }
+
+// Four signed int8 in `w`, bytes (b0, b1) or (b2, b3), to an exact f16 pair.
+// 0x64XX as f16 is 1024 + XX; biasing the byte by 0x80 maps x in [-128,127] to
+// 1152 + x, which is exact, and the packed subtraction of 1152 is exact too.
+__device__ __forceinline__ uint32_t i8pair_to_f16x2(uint32_t w_xor80, uint32_t sel) {
+  uint32_t biased = __builtin_amdgcn_perm(0x64646464u, w_xor80, sel);
+  f16x2 h = __builtin_bit_cast(f16x2, biased);
+  const f16x2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  return __builtin_bit_cast(uint32_t, h + bias);
+}
+// Byte `e` of words a (low half) and b (high half) as an exact f16 pair.
+__device__ __forceinline__ uint32_t i8gather_to_f16x2(uint32_t a, uint32_t b, int e) {
+  // selector: result byte0 = a.byte(e), byte1 = 0, byte2 = b.byte(e), byte3 = 0
+  const uint32_t sel = (uint32_t)e | 0x0c00u | ((uint32_t)(4 + e) << 16) | 0x0c000000u;
+  uint32_t w = __builtin_amdgcn_perm(b, a, sel) ^ 0x64806480u;
+  f16x2 h = __builtin_bit_cast(f16x2, w);
+  const f16x2 bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  return __builtin_bit_cast(uint32_t, h + bias);
+}
+// Half `hsel` (0 = low, 1 = high) of words a and b as one packed pair.
+__device__ __forceinline__ uint32_t gather16(uint32_t a, uint32_t b, int hsel) {
+  return __builtin_amdgcn_perm(b, a, hsel ? 0x07060302u : 0x05040100u);
+}
+
+// ---------------------------------------------------------------------- MFMA
+
+__device__ __forceinline__ f32x4 mfma16x16x32(F16, u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32(BF16, u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+// 16x16x16: A/B hold 4 elements (2 words) per lane, k = 4*(lane/16) + i.
+__device__ __forceinline__ f32x4 mfma16x16x16(F16, u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                               __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x16(BF16, u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                   __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ wave ops
+
+__device__ __forceinline__ float wave_max_xor16_32(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ float wave_sum_xor16_32(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ------------------------------------------------------------------- loads
+
+template <int BYTES>
+struct Raw {
+  static_assert(BYTES % 4 == 0 || BYTES == 2 || BYTES == 1, "raw size");
+  static constexpr int W = BYTES >= 4 ? BYTES / 4 : 1;
+  uint32_t w[W];
+};
+
+template <int BYTES>
+__device__ __forceinline__ void load_raw(Raw<BYTES>& r, const char* p) {
+  if constexpr (BYTES % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < BYTES / 16; ++i) {
+      u32x4 x = *(const u32x4*)(p + 16 * i);
+      r.w[4 * i + 0] = x[0];
+      r.w[4 * i + 1] = x[1];
+      r.w[4 * i + 2] = x[2];
+      r.w[4 * i + 3] = x[3];
+    }
+  } else if constexpr (BYTES == 8) {
+    u32x2 x = *(const u32x2*)p;
+    r.w[0] = x[0];
+    r.w[1] = x[1];
+  } else if constexpr (BYTES == 4) {
+    r.w[0] = *(const uint32_t*)p;
+  } else {
+    static_assert(BYTES % 16 == 0 || BYTES == 8 || BYTES == 4, "unsupported load width");
+  }
+}
+
+template <int BYTES>
+__device__ __forceinline__ void zero_raw(Raw<BYTES>& r) {
+#pragma unroll
+  for (int i = 0; i < Raw<BYTES>::W; ++i) r.w[i] = 0u;
+}
+
+}  // namespace sia

@@ -1,0 +1,193 @@
+"""Decode attention (Tq == 1) entry points with the reference's signatures.
+
+Each function is a drop-in for the reference function of the same name and
+keeps its argument meaning, output layout and assertion behaviour; the work is
+done by the gfx950 HIP kernels behind ``include/sia_attention.h``:
+
+=================================  =================================================
+this module                        reference
+=================================  =================================================
+attention_flash_decode             kernels/flash_decode_kernel.py:119-160
+attention_flash_decode_int8        kernels/flash_decode_int8_kernel.py:121-167
+paged_attention_flash_decode       kernels/paged_flash_decode_kernel.py:107-152
+gqa_int8_flash_decode              kernels/paged_flash_decode_int8_gqa_kernel.py:100-124
+paged_gqa_int8_flash_decode        (new: paged pool + int8 + GQA, BASELINE configs 3/5)
+=================================  =================================================
+
+Differences that only widen the reference's contract:
+
+* ``kv_len`` may also be a ``(B,)`` int32 tensor (one length per sequence);
+  a ``(1,)`` or ``()`` tensor keeps the reference's shared length.
+* Long contexts are split across work-groups (split-K) and merged by a
+  second kernel; the split is chosen on the device from ``kv_len``, so one
+  captured HIP graph stays valid for every length.  Callers can pin the split
+  with :func:`decode_options` (tests use it; the default is automatic).
+"""
+
+from __future__ import annotations
+
+import contextlib
+import ctypes
+import threading
+
+import torch
+
+from . import _lib
+
+_HEAD_DIMS = (16, 32, 64, 128, 256)
+_tls = threading.local()
+_ws_cache: dict = {}
+
+
+def _fail(cond: bool, msg: str) -> None:
+    """The reference wrappers assert; raise the same AssertionError (even under -O)."""
+    if not cond:
+        raise AssertionError(msg)
+
+
+@contextlib.contextmanager
+def decode_options(tiles_per_split: int = 0):
+    """Force the split-K size (in 16-token tiles) for decode calls in this block."""
+    prev = getattr(_tls, "tiles_per_split", 0)
+    _tls.tiles_per_split = int(tiles_per_split)
+    try:
+        yield
+    finally:
+        _tls.tiles_per_split = prev
+
+
+def decode_workspace_size(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
+    """Bytes of split-K workspace a decode call of this geometry needs."""
+    key = (batch, num_q_heads, num_kv_heads, head_dim, torch.cuda.current_device())
+    n = _ws_cache.get(key)
+    if n is None:
+        h = _lib.require_library()
+        out = ctypes.c_size_t(0)
+        _lib.check(h.sia_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, ctypes.byref(out)))
+        n = _ws_cache[key] = int(out.value)
+    return n
+
+
+def _kv_len_tensor(kv_len, device: torch.device) -> torch.Tensor:
+    if isinstance(kv_len, torch.Tensor):
+        if kv_len.dtype != torch.int32:
+            raise ValueError("kv_len must be an int32 tensor")
+        if kv_len.device != device:
+            raise ValueError("kv_len must live on the same device as q")
+        return kv_len
+    return torch.tensor([int(kv_len)], dtype=torch.int32, device=device)
+
+
+def _options():
+    tps = getattr(_tls, "tiles_per_split", 0)
+    if not tps:
+        return None
+    o = _lib.DecodeOptions()
+    o.tiles_per_split = tps
+    return ctypes.byref(o)
+
+
+def _run(fn_name: str, q: torch.Tensor, tensors, scalars, Hkv: int, sm_scale: float) -> torch.Tensor:
+    h = _lib.require_library()
+    if not q.is_cuda:
+        raise ValueError("decode attention runs on the GPU: q must be a CUDA (HIP) tensor")
+    B, Hq, Tq, D = q.shape
+    with torch.cuda.device(q.device):
+        out = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
+        ws_bytes = decode_workspace_size(B, Hq, Hkv, D)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        descs = [_lib.desc(t) for t in tensors]
+        args = [ctypes.byref(d) for d in descs]
+        out_desc = _lib.desc(out)
+        rc = getattr(h, fn_name)(
+            *args, *scalars, ctypes.c_float(sm_scale), ctypes.byref(out_desc),
+            ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws_bytes), _options(),
+            ctypes.c_void_p(_lib.stream_handle(q.device)))
+        _lib.check(rc)
+    return out
+
+
+def _common(q: torch.Tensor, k: torch.Tensor, sm_scale):
+    B, Hq, Tq, D = q.shape
+    _fail(Tq == 1, "decode kernel expects a single query position")
+    _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
+    return (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
+
+
+def attention_flash_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_len,
+                           sm_scale: float | None = None) -> torch.Tensor:
+    """Decode attention over a contiguous fp16/bf16 cache.
+
+    q: (B, Hq, 1, D); k, v: (B, Hkv, S, D) (views into the preallocated cache);
+    kv_len: int32 device tensor, (1,)/() shared or (B,) per sequence.
+    Returns (B, 1, Hq, D) token-major in q's dtype.
+    """
+    scale = _common(q, k, sm_scale)
+    kl = _kv_len_tensor(kv_len, q.device)
+    return _run("sia_attention_flash_decode", q, [q, k, v, kl], [], k.shape[1], scale)
+
+
+def attention_flash_decode_int8(q: torch.Tensor, k_int8: torch.Tensor, v_int8: torch.Tensor,
+                                k_scale: torch.Tensor, v_scale: torch.Tensor, kv_len,
+                                sm_scale: float | None = None) -> torch.Tensor:
+    """Decode attention over an int8 cache with per-(b, kv-head, pos) scales.
+
+    k_int8, v_int8: (B, Hkv, S, D) int8; k_scale, v_scale: (B, Hkv, S) fp32 or fp16.
+    """
+    scale = _common(q, k_int8, sm_scale)
+    kl = _kv_len_tensor(kv_len, q.device)
+    return _run("sia_attention_flash_decode_int8", q, [q, k_int8, v_int8, k_scale, v_scale, kl], [],
+                k_int8.shape[1], scale)
+
+
+def gqa_int8_flash_decode(q, k_int8, v_int8, k_scale, v_scale, kv_len, sm_scale=None):
+    """GQA-grouped int8 decode: q (B, Hq, 1, D); k/v_int8 (B, Hkv, S, D); scales (B, Hkv, S).
+
+    Every decode kernel here already reads each KV head once for its whole
+    query-head group, so this shares the int8 kernel.
+    """
+    scale = _common(q, k_int8, sm_scale)
+    kl = _kv_len_tensor(kv_len, q.device)
+    return _run("sia_gqa_int8_flash_decode", q, [q, k_int8, v_int8, k_scale, v_scale, kl], [],
+                k_int8.shape[1], scale)
+
+
+def paged_attention_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                                 block_table: torch.Tensor, kv_len, page_size: int,
+                                 sm_scale: float | None = None) -> torch.Tensor:
+    """Decode attention over a paged fp16/bf16 pool.
+
+    k_pool, v_pool: (num_blocks, Hkv, page_size, D); block_table: (B, max_blocks)
+    int32 logical->physical page ids.
+    """
+    B, Hq, Tq, D = q.shape
+    _, Hkv, P, _ = k_pool.shape
+    _fail(Tq == 1, "decode kernel expects a single query position")
+    _fail(P == page_size, f"k_pool page dim {P} != page_size {page_size}")
+    _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
+    scale = (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
+    kl = _kv_len_tensor(kv_len, q.device)
+    return _run("sia_paged_attention_flash_decode", q, [q, k_pool, v_pool, block_table, kl],
+                [ctypes.c_int32(page_size)], Hkv, scale)
+
+
+def paged_gqa_int8_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                                k_scale_pool: torch.Tensor, v_scale_pool: torch.Tensor,
+                                block_table: torch.Tensor, kv_len, page_size: int,
+                                sm_scale: float | None = None) -> torch.Tensor:
+    """Paged INT8-KV GQA decode.
+
+    k_pool, v_pool: (num_blocks, Hkv, page_size, D) int8; k_scale_pool,
+    v_scale_pool: (num_blocks, Hkv, page_size) fp32 or fp16; block_table
+    (B, max_blocks) int32; kv_len (1,)/() or (B,) int32.
+    """
+    B, Hq, Tq, D = q.shape
+    _, Hkv, P, _ = k_pool.shape
+    _fail(Tq == 1, "decode kernel expects a single query position")
+    _fail(P == page_size, f"k_pool page dim {P} != page_size {page_size}")
+    _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
+    scale = (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
+    kl = _kv_len_tensor(kv_len, q.device)
+    return _run("sia_paged_gqa_int8_flash_decode", q,
+                [q, k_pool, v_pool, k_scale_pool, v_scale_pool, block_table, kl],
+                [ctypes.c_int32(page_size)], Hkv, scale)

@@ -1,0 +1,87 @@
+"""CPU checks of the C ABI: the library loads and exports every declared symbol.
+
+No kernel is launched here (there may be no GPU); only pure host functions
+(ABI version, status strings, workspace sizing, argument validation) run.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import glob
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+import torch  # noqa: F401  (torch's HIP runtime must be loaded before the library)
+
+from conftest import ROOT, load_pkg
+
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
+
+
+def declared_symbols():
+    names = set()
+    for h in HEADERS:
+        text = open(h).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(sia_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    pkg = load_pkg()
+    path = pkg.library_path()
+    if not os.path.exists(path):  # build on the CPU (hipcc cross-compiles gfx950)
+        build = os.path.join(ROOT, "simple-inference-autoresearch_amd", "csrc", "build.py")
+        subprocess.run([sys.executable, build], check=True)
+    return pkg.load_library()
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    for must in ("sia_attention_flash_decode", "sia_attention_flash_decode_int8",
+                 "sia_paged_attention_flash_decode", "sia_gqa_int8_flash_decode",
+                 "sia_paged_gqa_int8_flash_decode", "sia_decode_workspace_size"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [n for n in declared_symbols() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_header():
+    pkg = load_pkg()
+    assert sorted(pkg.exported_symbols()) == declared_symbols()
+
+
+def test_host_only_functions(lib):
+    assert lib.sia_abi_version() == 1
+    assert lib.sia_status_string(0) == b"ok"
+    assert lib.sia_status_string(-1) == b"invalid argument"
+    n = ctypes.c_size_t(0)
+    assert lib.sia_decode_workspace_size(64, 32, 8, 128, ctypes.byref(n)) == 0
+    assert n.value > 64 * 8 * 4 * 130 * 4  # at least one fp32 partial per (sequence, kv head)
+    assert lib.sia_decode_workspace_size(2, 7, 2, 128, ctypes.byref(n)) == -1   # 7 % 2 != 0
+    assert b"multiple" in lib.sia_last_error_message()
+
+
+def test_null_arguments_are_rejected_without_launching(lib):
+    rc = lib.sia_attention_flash_decode(None, None, None, None, ctypes.c_float(0.1), None, None, 0, None, None)
+    assert rc == -1
+
+
+def test_no_cpu_fallback(monkeypatch):
+    """Without the HIP library (or without a GPU) the product path raises."""
+    pkg = load_pkg()
+    from importlib import import_module
+    lib_mod = import_module("simple-inference-autoresearch_amd._lib")
+    monkeypatch.setattr(lib_mod, "LIB_PATH", "/nonexistent/libsia_attention.so")
+    monkeypatch.setattr(lib_mod, "_lib", None)
+    q = torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16)
+    with pytest.raises(pkg.LibraryMissing):
+        pkg.attention_flash_decode(q, k, k, torch.tensor([16], dtype=torch.int32))
