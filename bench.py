@@ -1,0 +1,272 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Headline (BASELINE.json ``metric``): paged INT8-KV GQA decode, config 3 --
+batch 64, 32 Q / 8 KV heads, head_dim 128, page 16, every context 8192,
+int8 K/V with per-token-per-head fp32 scales, bf16 queries.  One step is one
+decode call over the whole batch with every input already resident in HBM.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-others]
+
+Prints ONE JSON line.  ``value`` is the achieved algorithmic HBM throughput of
+the whole call (GB/s); ``roofline`` refers to the dominant kernel
+(``decode_main``), timed with HIP events recorded by the library on the launch
+stream around that kernel alone; ``cpu_baseline`` times the reference's CPU
+torch path (restated in ``oracle/eager_path.py``) on a bounded sample of the
+same workload.  ``other_configs`` carries configs 2 and 5 (decode) and 4
+(prefill) measured the same way when available.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+PKG_NAME = "simple-inference-autoresearch_amd"
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+METRIC = "paged INT8-KV GQA decode: µs/call + achieved HBM GB/s (% of peak), 1 GPU"
+
+
+def _pkg():
+    return importlib.import_module(PKG_NAME)
+
+
+def _syn():
+    return importlib.import_module(PKG_NAME + ".synthetic")
+
+
+def run_decode(pkg, case):
+    if case.is_int8:
+        return pkg.paged_gqa_int8_flash_decode(case.q, case.k_pool, case.v_pool, case.k_scale, case.v_scale,
+                                               case.block_table, case.kv_len, case.page_size)
+    return pkg.paged_attention_flash_decode(case.q, case.k_pool, case.v_pool, case.block_table, case.kv_len,
+                                            case.page_size)
+
+
+def time_decode(pkg, case, steps: int, warmup: int):
+    """W untimed calls, then exactly `steps` timed calls.
+
+    Returns (ms per call for the whole call, list of main-kernel ms per call).
+    """
+    import torch
+
+    for _ in range(warmup):
+        run_decode(pkg, case)
+    begins = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in begins + ends:      # create the underlying hipEvents before handing them to the library
+        e.record()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(steps):
+        with pkg.decode_options(main_events=(begins[i], ends[i])):
+            run_decode(pkg, case)
+    t1.record()
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    kern = [b.elapsed_time(e) for b, e in zip(begins, ends)]
+    return total_ms / steps, kern
+
+
+def cpu_baseline(case, target_s: float):
+    """Time the reference's CPU path (gather pages, dequantise, repeat_interleave + SDPA).
+
+    Bounded sample: a few whole sequences of the same batch are copied to the
+    host and run repeatedly for about `target_s` seconds; the reported rate is
+    the same algorithmic-bytes metric over the sequences processed.
+    """
+    import torch
+
+    from oracle import eager_path as E
+
+    rows = [0, 1, 2, 3]
+    B, Hq, _, D = case.q.shape
+    Hkv, page = case.k_pool.shape[1], case.page_size
+    # pull just these sequences' pages to the host and renumber them
+    pages, bts = [], []
+    base = 0
+    for r in rows:
+        n = math.ceil(case.ctx[r] / page)
+        pages.append(case.block_table[r, :n].long())
+        bts.append(torch.arange(base, base + n, dtype=torch.int32))
+        base += n
+    idx = torch.cat(pages)
+    kp, vp = case.k_pool[idx].cpu(), case.v_pool[idx].cpu()
+    ksp, vsp = case.k_scale[idx].cpu(), case.v_scale[idx].cpu()
+    maxn = max(len(b) for b in bts)
+    bt = torch.zeros(len(rows), maxn, dtype=torch.int32)
+    for i, b in enumerate(bts):
+        bt[i, :len(b)] = b
+    q = case.q[rows].float().cpu()
+    lens = [case.ctx[r] for r in rows]
+    sub_rows = list(range(len(rows)))
+    for _ in range(2):  # warm-up
+        E.eager_paged_int8_decode(q, kp, vp, ksp, vsp, bt, lens, page, batch_rows=sub_rows)
+    reps, t_start = 0, time.perf_counter()
+    times = []
+    while True:
+        t = time.perf_counter()
+        E.eager_paged_int8_decode(q, kp, vp, ksp, vsp, bt, lens, page, batch_rows=sub_rows)
+        times.append(time.perf_counter() - t)
+        reps += 1
+        if time.perf_counter() - t_start >= target_s and reps >= 5:
+            break
+    tokens = sum(lens)
+    sample_bytes = (tokens * Hkv * D * 2 + tokens * Hkv * 4 * 2 + 2 * len(rows) * Hq * D * 2
+                    + 4 * sum(len(b) for b in bts))
+    med = statistics.median(times)
+    try:
+        model = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except (OSError, StopIteration):
+        model = platform.processor()
+    return {
+        "value": round(sample_bytes / med / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config-3 sequences {rows} ({tokens} tokens, {sample_bytes} algorithmic bytes) through "
+                   f"oracle/eager_path.py (gather pages, dequantise, repeat_interleave + SDPA, fp32), "
+                   f"median of {reps} reps over {time.perf_counter() - t_start:.1f}s"),
+        "us_per_sample": round(med * 1e6, 1),
+        "host_cpu": model,
+        "os_cpu_count": os.cpu_count(),
+    }
+
+
+def bench_decode_config(pkg, case, steps, warmup):
+    syn = _syn()
+    ms, kern = time_decode(pkg, case, steps, warmup)
+    nbytes = syn.decode_bytes(case)
+    kern_ms = statistics.mean(kern)
+    return {
+        "us_per_call": round(ms * 1e3, 2),
+        "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "main_kernel_us": round(kern_ms * 1e3, 2),
+        "main_kernel_GBps": round(nbytes / (kern_ms * 1e-3) / 1e9, 1),
+        "frac_of_hbm_peak": round(nbytes / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes": nbytes,
+    }
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), or None."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--no-others", action="store_true", help="skip configs 2, 4 and 5")
+    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg5"],
+                   help="decode config to run as the headline (profiling runs)")
+    args = p.parse_args(argv)
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures the attention hot path on ONE GPU; multi-GPU runs are out of scope "
+              "for this build (each GPU box has one MI355X). Run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    pkg = _pkg()
+    pkg.require_library()
+    syn = _syn()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    case = getattr(syn, args.config)(dev)
+    torch.cuda.synchronize()
+    print(f"[bench] {args.config}: inputs resident ({syn.decode_bytes(case)/1e9:.3f} GB algorithmic)",
+          file=sys.stderr, flush=True)
+    head = bench_decode_config(pkg, case, args.steps, args.warmup)
+    print(f"[bench] {args.config}: {head}", file=sys.stderr, flush=True)
+
+    result = {
+        "metric": METRIC,
+        "value": head["GBps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call"] / 1e3, 5),
+        "us_per_call": head["us_per_call"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 K/V, bf16 q/out, fp32 softmax/accumulate",
+        "data": "synthetic (seeded N(0,1) K/V quantised per token per head; random page permutation)",
+        "config": {
+            "workload": {"cfg2": "config 2: paged fp16 decode B16 ctx U[256,4096]",
+                         "cfg3": "config 3: paged INT8-KV GQA decode B64 ctx 8192",
+                         "cfg5": "config 5: split-K paged INT8-KV decode B256 Hq64 lognormal ctx"}[args.config],
+            "batch": int(case.q.shape[0]), "q_heads": int(case.q.shape[1]), "kv_heads": int(case.k_pool.shape[1]),
+            "head_dim": int(case.q.shape[3]), "page_size": case.page_size, "contexts": f"sum {sum(case.ctx)}",
+            "algorithmic_bytes": head["algorithmic_bytes"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": head["main_kernel_GBps"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": head["frac_of_hbm_peak"],
+            "traffic": None,
+            "kernel": "decode_main",
+            "kernel_us": head["main_kernel_us"],
+        },
+    }
+    tr = load_traffic(f"decode_main_{args.config}")
+    if tr is not None:
+        result["roofline"]["traffic"] = tr.get("hbm_bytes_per_launch")
+        result["roofline"]["traffic_source"] = tr.get("source")
+
+    if not args.no_others and args.config == "cfg3":
+        others = {}
+        del case
+        torch.cuda.empty_cache()
+        for name in ("cfg2", "cfg5"):
+            c = getattr(syn, name)(dev)
+            torch.cuda.synchronize()
+            others[name] = bench_decode_config(pkg, c, max(20, args.steps // 2), args.warmup)
+            print(f"[bench] {name}: {others[name]}", file=sys.stderr, flush=True)
+            del c
+            torch.cuda.empty_cache()
+        result["other_configs"] = others
+        case = None
+
+    if not args.no_cpu_baseline:
+        if case is None:
+            case = syn.cfg3(dev)
+        print("[bench] timing the CPU baseline sample", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -62,10 +62,13 @@ typedef struct sia_tensor {
   int64_t stride[SIA_MAX_DIMS];   /* in elements */
 } sia_tensor;
 
-/* Optional tuning knobs for the decode family; pass NULL for the defaults. */
+/* Optional knobs for the decode family; pass NULL for the defaults. */
 typedef struct sia_decode_options {
   int32_t tiles_per_split;  /* 0 = automatic; else force this many 16-token tiles per split-K item */
-  int32_t reserved[7];      /* must be zero */
+  int32_t reserved0;        /* must be zero */
+  void* main_begin_event;   /* optional hipEvent_t recorded on `stream` just before the main decode kernel */
+  void* main_end_event;     /* optional hipEvent_t recorded just after it (before the split-K reduction) */
+  int64_t reserved[4];      /* must be zero */
 } sia_decode_options;
 
 int sia_abi_version(void);

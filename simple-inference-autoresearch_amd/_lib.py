@@ -56,7 +56,13 @@ class SiaTensor(ctypes.Structure):
 
 
 class DecodeOptions(ctypes.Structure):
-    _fields_ = [("tiles_per_split", ctypes.c_int32), ("reserved", ctypes.c_int32 * 7)]
+    _fields_ = [
+        ("tiles_per_split", ctypes.c_int32),
+        ("reserved0", ctypes.c_int32),
+        ("main_begin_event", ctypes.c_void_p),
+        ("main_end_event", ctypes.c_void_p),
+        ("reserved", ctypes.c_int64 * 4),
+    ]
 
 
 _P = ctypes.POINTER(SiaTensor)

@@ -174,9 +174,12 @@ int prepare_table(const sia_tensor* bt, const Geometry& g, int page_size, Decode
 
 int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decode_options* opts, DecodeLaunch& L) {
   if (opts != nullptr) {
-    for (int i = 0; i < 7; ++i)
-      if (opts->reserved[i] != 0) return fail(SIA_ERR_INVALID_ARGUMENT, "sia_decode_options.reserved must be zero");
+    bool dirty = opts->reserved0 != 0;
+    for (int i = 0; i < 4; ++i) dirty |= opts->reserved[i] != 0;
+    if (dirty) return fail(SIA_ERR_INVALID_ARGUMENT, "sia_decode_options reserved fields must be zero");
     if (opts->tiles_per_split < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "tiles_per_split must be >= 0");
+    L.begin_event = (hipEvent_t)opts->main_begin_event;
+    L.end_event = (hipEvent_t)opts->main_end_event;
   }
   const size_t pb = plan_bytes(g.B);
   const size_t ib = item_bytes(g);
@@ -208,6 +211,7 @@ int decode_any(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, co
                float sm_scale, const sia_tensor* out, void* ws, size_t ws_bytes,
                const sia_decode_options* opts, void* stream, bool want_int8) {
   DecodeLaunch L;
+  memset(&L, 0, sizeof(L));
   Geometry g;
   int rc;
   if (k == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "k is NULL");

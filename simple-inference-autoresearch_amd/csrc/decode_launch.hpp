@@ -16,6 +16,8 @@ struct DecodeLaunch {
   int q_dtype;       // SIA_F16 / SIA_BF16 (also the output dtype)
   int scale_dtype;   // SIA_F32 / SIA_F16 (int8 only)
   hipStream_t stream;
+  hipEvent_t begin_event;   // optional, recorded around the main kernel
+  hipEvent_t end_event;
 };
 
 inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
@@ -31,9 +33,13 @@ int launch_decode_typed(DecodeLaunch& L) {
   int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
   if (occ <= 0) return fail(SIA_ERR_LAUNCH, "decode kernel does not fit on a CU (LDS %zu B)", lds);
   const int slots = device_info().cus * occ;
+  if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
+    return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
   hipLaunchKernelGGL(kmain, dim3(slots), dim3(NW * 64), lds, L.stream, L.a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode launch: %s", hipGetErrorString(e));
+  if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
+    return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
   const int rows = L.a.B * L.a.Hq;
   hipLaunchKernelGGL((decode_reduce<D, QT>), dim3((rows + 3) / 4), dim3(256), 0, L.stream, L.a);
   e = hipGetLastError();

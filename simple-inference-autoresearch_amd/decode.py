@@ -46,14 +46,21 @@ def _fail(cond: bool, msg: str) -> None:
 
 
 @contextlib.contextmanager
-def decode_options(tiles_per_split: int = 0):
-    """Force the split-K size (in 16-token tiles) for decode calls in this block."""
-    prev = getattr(_tls, "tiles_per_split", 0)
+def decode_options(tiles_per_split: int = 0, main_events=None):
+    """Options for decode calls made in this block (this thread).
+
+    tiles_per_split: force the split-K size in 16-token tiles (0 = automatic).
+    main_events: optional ``(begin, end)`` pair of ``torch.cuda.Event``; the
+        library records them on the launch stream around the main decode
+        kernel (excluding the split-K reduction), for kernel timing.
+    """
+    prev = (getattr(_tls, "tiles_per_split", 0), getattr(_tls, "main_events", None))
     _tls.tiles_per_split = int(tiles_per_split)
+    _tls.main_events = main_events
     try:
         yield
     finally:
-        _tls.tiles_per_split = prev
+        _tls.tiles_per_split, _tls.main_events = prev
 
 
 def decode_workspace_size(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
@@ -80,10 +87,14 @@ def _kv_len_tensor(kv_len, device: torch.device) -> torch.Tensor:
 
 def _options():
     tps = getattr(_tls, "tiles_per_split", 0)
-    if not tps:
+    ev = getattr(_tls, "main_events", None)
+    if not tps and ev is None:
         return None
     o = _lib.DecodeOptions()
     o.tiles_per_split = tps
+    if ev is not None:
+        o.main_begin_event = ev[0].cuda_event
+        o.main_end_event = ev[1].cuda_event
     return ctypes.byref(o)
 
 
