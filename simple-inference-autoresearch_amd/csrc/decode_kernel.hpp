@@ -40,6 +40,10 @@ namespace sia {
 
 constexpr int kTile = 16;          // tokens per MFMA tile
 constexpr int kTpsMin = 8;         // smallest split, in tiles
+// The running max is only raised when a score exceeds it by more than this
+// (log2 units), so p = 2^(s - m) <= 2^8: well inside f16/bf16 range, and the
+// rescale of (l, acc) almost never runs after the first tile.
+constexpr float kLazyMax = 8.0f;
 
 struct DecodeArgs {
   const char* q; int64_t q_sb, q_sh;                 // byte strides
@@ -177,39 +181,17 @@ struct Tile {
   float ks[4], vs[4];                                // int8 scales of tokens 4*grp + i
 };
 
-struct TileAddr {
-  const char* k; const char* v; const char* ks; const char* vs;
-  int valid;   // tokens of this tile that exist (0..16)
+// Byte offsets of this lane's operands inside one tile (constant per item).
+struct LaneOff {
+  uint32_t k;       // token lane16, elements [grp*D/4, +D/4)
+  uint32_t v[4];    // token 4*grp+i, elements [lane16*D/16, +D/16)
+  uint32_t ks, vs;  // scales of tokens 4*grp .. 4*grp+3
 };
 
-__device__ __forceinline__ TileAddr tile_addr(const DecodeArgs& a, int b, int hkv, int tile, int ntok) {
-  TileAddr t;
-  const int tok0 = tile * kTile;
-  int valid = ntok - tok0;
-  valid = valid < 0 ? 0 : (valid > kTile ? kTile : valid);
-  int64_t ok, ov, oks, ovs;
-  if (a.bt != nullptr) {
-    const int pidx = tile >> a.lg_tiles_per_page;
-    const int off = (tile - (pidx << a.lg_tiles_per_page)) * kTile;
-    int64_t phys = 0;
-    if (valid > 0) {
-      phys = a.bt[b * a.bt_sb + pidx * a.bt_sl];
-      if (phys < 0 || phys >= a.num_pages) { valid = 0; phys = 0; }  // never read outside the pool
-    }
-    ok = phys * a.k_s0 + hkv * a.k_sh + off * a.k_sn;
-    ov = phys * a.v_s0 + hkv * a.v_sh + off * a.v_sn;
-    oks = phys * a.ks_s0 + hkv * a.ks_sh + off * a.ks_sn;
-    ovs = phys * a.vs_s0 + hkv * a.vs_sh + off * a.vs_sn;
-  } else {
-    ok = b * a.k_s0 + hkv * a.k_sh + tok0 * a.k_sn;
-    ov = b * a.v_s0 + hkv * a.v_sh + tok0 * a.v_sn;
-    oks = b * a.ks_s0 + hkv * a.ks_sh + tok0 * a.ks_sn;
-    ovs = b * a.vs_s0 + hkv * a.vs_sh + tok0 * a.vs_sn;
-  }
-  t.k = a.k + ok; t.v = a.v + ov; t.ks = a.ks + oks; t.vs = a.vs + ovs;
-  t.valid = valid;
-  return t;
-}
+// Uniform base pointers of one tile (scalar registers).
+struct TilePtr {
+  const char* k; const char* v; const char* ks; const char* vs;
+};
 
 template <class ST>
 __device__ __forceinline__ float load_scale(const char* p) {
@@ -217,35 +199,31 @@ __device__ __forceinline__ float load_scale(const char* p) {
   else return (float)*(const _Float16*)p;
 }
 
-// Load this lane's operands of one tile.  FULL: all 16 tokens exist and the
-// tile's page is valid, so no per-lane predicates are needed.
+// Load this lane's operands of one tile.  FULL: all 16 tokens exist, so no
+// per-lane predicate; otherwise tokens >= `valid` read as zero.
 template <int D, class KV, class ST, bool FULL>
-__device__ __forceinline__ void load_tile(const DecodeArgs& a, const TileAddr& t, Tile<D, KV, ST>& c,
-                                          int lane16, int grp) {
+__device__ __forceinline__ void load_tile(const DecodeArgs& a, const TilePtr& t, const LaneOff& o, int valid,
+                                          Tile<D, KV, ST>& c, int lane16, int grp) {
   using C = Tile<D, KV, ST>;
-  const char* kp = t.k + lane16 * a.k_sn + grp * C::KB;
-  if (FULL || lane16 < t.valid) load_raw<C::KB>(c.k, kp);
+  if (FULL || lane16 < valid) load_raw<C::KB>(c.k, t.k + o.k);
   else zero_raw<C::KB>(c.k);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int tok = 4 * grp + i;
-    const char* vp = t.v + tok * a.v_sn + lane16 * C::VB;
-    if (FULL || tok < t.valid) load_raw<C::VB>(c.v[i], vp);
+    if (FULL || 4 * grp + i < valid) load_raw<C::VB>(c.v[i], t.v + o.v[i]);
     else zero_raw<C::VB>(c.v[i]);
   }
   if constexpr (C::kInt8) {
     if (FULL && std::is_same<ST, F32>::value && a.scale_vec) {
-      const f32x4 k4 = *(const f32x4*)(t.ks + 4 * grp * a.ks_sn);
-      const f32x4 v4 = *(const f32x4*)(t.vs + 4 * grp * a.vs_sn);
+      const f32x4 k4 = *(const f32x4*)(t.ks + o.ks);
+      const f32x4 v4 = *(const f32x4*)(t.vs + o.vs);
 #pragma unroll
       for (int i = 0; i < 4; ++i) { c.ks[i] = k4[i]; c.vs[i] = v4[i]; }
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int tok = 4 * grp + i;
-        const bool ok = FULL || tok < t.valid;
-        c.ks[i] = ok ? load_scale<ST>(t.ks + tok * a.ks_sn) : 0.0f;
-        c.vs[i] = ok ? load_scale<ST>(t.vs + tok * a.vs_sn) : 0.0f;
+        const bool ok = FULL || 4 * grp + i < valid;
+        c.ks[i] = ok ? load_scale<ST>(t.ks + o.ks + i * (uint32_t)a.ks_sn) : 0.0f;
+        c.vs[i] = ok ? load_scale<ST>(t.vs + o.vs + i * (uint32_t)a.vs_sn) : 0.0f;
       }
     }
   }
@@ -336,7 +314,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
   float alpha = 1.0f;        // rescales l and acc when the running max grows
   float acc_alpha = 1.0f;    // extra factor for acc alone (int8 value-scale headroom)
   bool rescale = false;
-  if (__any(lmax > st.m)) {
+  if (__any(lmax > st.m + kLazyMax)) {
     const float m_new = fmaxf(st.m, wave_max_xor16_32(lmax));
     alpha = fast_exp2(st.m - m_new);
     st.m = m_new;
@@ -348,7 +326,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
 
   u32x2 pop, pop_lo;
   if constexpr (kInt8) {
-    // P' = p * s_v * 2^-sexp stays < 2^12 since 2^sexp tracks the largest s_v.
+    // P' = p * s_v * 2^(4-sexp) stays < 2^12: p <= 2^kLazyMax and 2^sexp bounds every s_v seen.
     const float lv = fmaxf(fmaxf(c.vs[0], c.vs[1]), fmaxf(c.vs[2], c.vs[3]));
     if (__any(lv > ldexpf(1.0f, st.sexp))) {
       const float vmax = wave_max_xor16_32(lv);
@@ -357,7 +335,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
       st.sexp = e_new;
       rescale = true;
     }
-    const float rho = ldexpf(4096.0f, -st.sexp);
+    const float rho = ldexpf(16.0f, -st.sexp);
     pop[0] = pack2(F16{}, p[0] * (c.vs[0] * rho), p[1] * (c.vs[1] * rho));
     pop[1] = pack2(F16{}, p[2] * (c.vs[2] * rho), p[3] * (c.vs[3] * rho));
   } else {
@@ -451,16 +429,23 @@ __global__ __launch_bounds__(NW * 64) void decode_main(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int lane16 = lane & 15, grp = lane >> 4;
+  using TileT = Tile<D, KV, ST>;
+  LaneOff lo;
+  lo.k = (uint32_t)(lane16 * a.k_sn) + (uint32_t)(grp * TileT::KB);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) lo.v[i] = (uint32_t)((4 * grp + i) * a.v_sn) + (uint32_t)(lane16 * TileT::VB);
+  lo.ks = (uint32_t)(4 * grp * a.ks_sn);
+  lo.vs = (uint32_t)(4 * grp * a.vs_sn);
 
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
     // item -> (b, split, unit): b is the largest index with pre[b] <= item
-    int lo = 0, hi = a.B;
-    while (hi - lo > 1) { const int mid = (lo + hi) >> 1; if (pre[mid] <= item) lo = mid; else hi = mid; }
-    const int b = lo;
-    const int rem = item - pre[b];
+    int blo = 0, bhi = a.B;
+    while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= item) blo = mid; else bhi = mid; }
+    const int b = uniform(blo);
+    const int rem = uniform(item - pre[b]);
     const int split = rem / a.U, unit = rem - split * a.U;
     const int hkv = unit / a.HG, hg = unit - hkv * a.HG;
-    const int ntok = seq_tokens(a, b);
+    const int ntok = uniform(seq_tokens(a, b));
     const int ntile = (ntok + kTile - 1) / kTile;
     const int nsplit = (ntile + tps - 1) / tps;
     const int t_lo = split * tps;
@@ -477,31 +462,80 @@ __global__ __launch_bounds__(NW * 64) void decode_main(const DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < E; ++e) st.acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Wave w takes tiles t_lo + w, + NW, ...; full tiles are double-buffered,
-    // the sequence's partial last tile (if this wave owns it) comes after.
+    // Wave w takes tiles t_lo + w, + NW, ...: `nfull` full tiles (double-
+    // buffered) and possibly the sequence's partial last tile.
+    const bool paged = a.bt != nullptr;
+    const int t_first = t_lo + wave;
     const int t_full = min(t_hi, ntok / kTile);
-    int t = t_lo + wave;
+    const int nfull = t_first < t_full ? (t_full - t_first + NW - 1) / NW : 0;
+    const int nt = t_first < t_hi ? (t_hi - t_first + NW - 1) / NW : 0;
+    const int64_t rowk = paged ? 0 : (int64_t)b * a.k_s0, rowv = paged ? 0 : (int64_t)b * a.v_s0;
+    const int64_t rowks = paged ? 0 : (int64_t)b * a.ks_s0, rowvs = paged ? 0 : (int64_t)b * a.vs_s0;
+    const char* kb = a.k + rowk + (int64_t)hkv * a.k_sh;
+    const char* vb = a.v + rowv + (int64_t)hkv * a.v_sh;
+    const char* ksb = a.ks + rowks + (int64_t)hkv * a.ks_sh;
+    const char* vsb = a.vs + rowvs + (int64_t)hkv * a.vs_sh;
+    const int tpp_mask = (1 << a.lg_tiles_per_page) - 1;
+    // tile k of this wave (k uniform) -> base pointers; `pg` holds the page ids
+    // of tiles [w0, w0+64) in lanes 0..63.
+    auto tile_ptr = [&](int t, int phys) {
+      TilePtr tp;
+      int64_t ok, ov, oks, ovs;
+      if (paged) {
+        const int off = (t & tpp_mask) * kTile;
+        ok = (int64_t)phys * a.k_s0 + off * a.k_sn;
+        ov = (int64_t)phys * a.v_s0 + off * a.v_sn;
+        oks = (int64_t)phys * a.ks_s0 + off * a.ks_sn;
+        ovs = (int64_t)phys * a.vs_s0 + off * a.vs_sn;
+      } else {
+        ok = (int64_t)t * kTile * a.k_sn;
+        ov = (int64_t)t * kTile * a.v_sn;
+        oks = (int64_t)t * kTile * a.ks_sn;
+        ovs = (int64_t)t * kTile * a.vs_sn;
+      }
+      tp.k = kb + ok; tp.v = vb + ov; tp.ks = ksb + oks; tp.vs = vsb + ovs;
+      return tp;
+    };
+    auto page_ids = [&](int w0, int wn) {
+      int pg = 0;
+      if (paged && lane < wn) {
+        const int t = t_first + (w0 + lane) * NW;
+        pg = a.bt[(int64_t)b * a.bt_sb + (int64_t)(t >> a.lg_tiles_per_page) * a.bt_sl];
+        pg = ((unsigned)pg < (unsigned long long)a.num_pages) ? pg : 0;   // never read outside the pool
+      }
+      return pg;
+    };
     Tile<D, KV, ST> bufA, bufB;
-    if (t < t_full) load_tile<D, KV, ST, true>(a, tile_addr(a, b, hkv, t, ntok), bufA, lane16, grp);
-    while (t < t_full) {
-      int nx = t + NW;
-      if (nx < t_full) load_tile<D, KV, ST, true>(a, tile_addr(a, b, hkv, nx, ntok), bufB, lane16, grp);
-      compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, t, ntok, grp, st);
-      t = nx;
-      if (t >= t_full) break;
-      nx = t + NW;
-      if (nx < t_full) load_tile<D, KV, ST, true>(a, tile_addr(a, b, hkv, nx, ntok), bufA, lane16, grp);
-      compute_tile<D, KV, QT, ST, true>(bufB, qop, qop_lo, qmul, t, ntok, grp, st);
-      t = nx;
+    for (int w0 = 0; w0 < nfull; w0 += 64) {
+      const int wn = min(64, nfull - w0);
+      const int pg = page_ids(w0, wn);
+      int k = 0;
+      load_tile<D, KV, ST, true>(a, tile_ptr(t_first + w0 * NW, __builtin_amdgcn_readlane(pg, 0)), lo, 16,
+                                 bufA, lane16, grp);
+      while (true) {
+        if (k + 1 < wn)
+          load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * NW, __builtin_amdgcn_readlane(pg, k + 1)),
+                                     lo, 16, bufB, lane16, grp);
+        compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, 0, ntok, grp, st);
+        if (++k >= wn) break;
+        if (k + 1 < wn)
+          load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * NW, __builtin_amdgcn_readlane(pg, k + 1)),
+                                     lo, 16, bufA, lane16, grp);
+        compute_tile<D, KV, QT, ST, true>(bufB, qop, qop_lo, qmul, 0, ntok, grp, st);
+        if (++k >= wn) break;
+      }
     }
-    if (t < t_hi) {  // the sequence's partial last tile
-      load_tile<D, KV, ST, false>(a, tile_addr(a, b, hkv, t, ntok), bufA, lane16, grp);
+    if (nt > nfull) {  // the sequence's partial last tile belongs to this wave
+      const int t = t_first + nfull * NW;
+      const int pg = page_ids(nfull, 1);
+      load_tile<D, KV, ST, false>(a, tile_ptr(t, __builtin_amdgcn_readlane(pg, 0)), lo, ntok - t * kTile,
+                                  bufA, lane16, grp);
       compute_tile<D, KV, QT, ST, false>(bufA, qop, qop_lo, qmul, t, ntok, grp, st);
     }
 
     // ---- merge the NW waves through LDS
     const float lsum = wave_sum_xor16_32(st.l);
-    const float unscale = std::is_same<KV, I8>::value ? ldexpf(1.0f, st.sexp - 12) : 1.0f;
+    const float unscale = std::is_same<KV, I8>::value ? ldexpf(1.0f, st.sexp - 4) : 1.0f;
     if (live) {
       float* dst = l_acc + (wave * a.G16 + lane16) * D + grp * (D / 4);
 #pragma unroll
