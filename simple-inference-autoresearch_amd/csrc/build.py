@@ -41,9 +41,18 @@ def sources():
     return sorted(f for f in os.listdir(HERE) if f.endswith((".hip", ".cpp")))
 
 
+# Extra flags per source: the decode kernels keep their MFMA accumulators in
+# VGPRs (no AGPR round trips around the online-softmax rescale).
+EXTRA_FLAGS = {
+    "decode_f16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "decode_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "decode_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def compile_one(src: str, verbose: bool):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [HIPCC, *COMMON_FLAGS, *EXTRA_FLAGS.get(src, []), "-c", os.path.join(HERE, src), "-o", obj]
     t0 = time.time()
     r = subprocess.run(cmd, capture_output=True, text=True)
     dt = time.time() - t0

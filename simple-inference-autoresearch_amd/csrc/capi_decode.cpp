@@ -18,17 +18,19 @@ constexpr int kPlanHeader = 4;
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct Geometry {
-  int B, Hq, Hkv, D, G, HG, U, G16;
+  int B, Hq, Hkv, D, G, HG, U, UB, G16;
 };
 
 size_t plan_bytes(int B) { return (size_t)round_up((int64_t)(kPlanHeader + B + 1) * 4, 256); }
-size_t item_bytes(const Geometry& g) { return (size_t)g.G16 * (g.D + 2) * 4; }
+// One item holds a partial for each of its kDecodeWaves unit slots.
+size_t item_bytes(const Geometry& g) { return (size_t)kDecodeWaves * g.G16 * (g.D + 2) * 4; }
 
-// Items the workspace must be able to hold: at most ~4 per persistent
-// work-group plus one per (sequence, unit) (see plan_items in decode_kernel.hpp).
+// Items the workspace must be able to hold: the split planner keeps the item
+// count near a few per persistent work-group (at most 4 groups per CU), plus
+// one per (sequence, unit block) (see plan_items in decode_kernel.hpp).
 int64_t wanted_items(const Geometry& g) {
   const int cus = device_info().cus > 0 ? device_info().cus : 256;
-  return 4LL * cus * 8 + (int64_t)g.B * g.U + 64;
+  return 8LL * cus * 4 + (int64_t)g.B * g.UB + 64;
 }
 
 int geometry(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, Geometry& g) {
@@ -42,6 +44,7 @@ int geometry(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, Geometry& g) {
   g.G = (int)(Hq / Hkv);
   g.HG = (g.G + 15) / 16;
   g.U = g.Hkv * g.HG;
+  g.UB = g.U >= kDecodeWaves ? (g.U + kDecodeWaves - 1) / kDecodeWaves : 1;
   g.G16 = g.G < 16 ? g.G : 16;
   return SIA_OK;
 }
@@ -94,7 +97,7 @@ int prepare_common(const sia_tensor* q, const sia_tensor* kv_len, const sia_tens
   a.out = (char*)out->data; a.o_sb = bstride(out, 0); a.o_sh = bstride(out, 2);
   a.kv_len = (const int32_t*)kv_len->data;
   a.kv_per_seq = (n == g.B && g.B > 1) ? 1 : 0;
-  a.B = g.B; a.Hq = g.Hq; a.Hkv = g.Hkv; a.G = g.G; a.HG = g.HG; a.U = g.U; a.G16 = g.G16;
+  a.B = g.B; a.Hq = g.Hq; a.Hkv = g.Hkv; a.G = g.G; a.HG = g.HG; a.U = g.U; a.UB = g.UB; a.G16 = g.G16;
   a.qk_scale = sm_scale * 1.4426950408889634f;
   L.D = g.D;
   L.q_dtype = q->dtype;
@@ -183,16 +186,16 @@ int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decod
   }
   const size_t pb = plan_bytes(g.B);
   const size_t ib = item_bytes(g);
-  if (ws == nullptr || bytes < pb + ib * (size_t)g.B * g.U || !aligned16(ws))
+  if (ws == nullptr || bytes < pb + ib * (size_t)g.B * g.UB || !aligned16(ws))
     return fail(SIA_ERR_WORKSPACE, "decode workspace missing, misaligned or smaller than %zu bytes",
-                pb + ib * (size_t)g.B * g.U);
+                pb + ib * (size_t)g.B * g.UB);
   int64_t items = (int64_t)((bytes - pb) / ib);
   if (items > 0x7fffffff) items = 0x7fffffff;
   DecodeArgs& a = L.a;
   a.ws_plan = (int32_t*)ws;
   a.max_items = (int32_t)items;
   a.ws_ml = (float*)((char*)ws + pb);
-  a.ws_acc = a.ws_ml + (size_t)items * g.G16 * 2;
+  a.ws_acc = a.ws_ml + (size_t)items * kDecodeWaves * g.G16 * 2;
   a.tps_force = opts ? opts->tiles_per_split : 0;
   return SIA_OK;
 }

@@ -57,7 +57,7 @@ struct DecodeArgs {
   int32_t lg_tiles_per_page;                         // page_size = 16 << lg
   const int32_t* kv_len; int32_t kv_per_seq;
   int32_t cap_tokens;                                // S (contiguous) or max_blocks*page_size
-  int32_t B, Hq, Hkv, G, HG, U;                      // U = Hkv*HG units per sequence
+  int32_t B, Hq, Hkv, G, HG, U, UB;                  // U = Hkv*HG units per sequence, UB unit blocks per item row
   float qk_scale;                                    // sm_scale * log2(e)
   float* ws_acc; float* ws_ml; int32_t* ws_plan; int32_t max_items; int32_t G16;
   int32_t tps_force;
@@ -97,14 +97,14 @@ __device__ __forceinline__ void block_sum_max(long long& sum, int& mx, int* red)
 
 // Exclusive scan of cnt[0..B) into pre[0..B] (pre[B] = total), in LDS.
 template <int NW>
-__device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pre, int* red) {
+__device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pre, int* red, int UB) {
   const int T = NW * 64, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (a.B + T - 1) / T;
   const int b0 = tid * per;
   int local = 0;
   for (int i = 0; i < per; ++i) {
     int b = b0 + i;
-    if (b < a.B) local += ((seq_tiles(a, b) + tps - 1) / tps) * a.U;
+    if (b < a.B) local += ((pre[b] + tps - 1) / tps) * UB;
   }
   int incl = local;
 #pragma unroll
@@ -121,8 +121,9 @@ __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pr
   for (int i = 0; i < per; ++i) {
     int b = b0 + i;
     if (b < a.B) {
+      const int cnt = pre[b];
       pre[b] = run;
-      run += ((seq_tiles(a, b) + tps - 1) / tps) * a.U;
+      run += ((cnt + tps - 1) / tps) * UB;
     }
   }
   if (tid == T - 1) pre[a.B] = run;
@@ -131,39 +132,76 @@ __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pr
 
 // Decide tiles-per-split from the device-side lengths and build the item
 // prefix (items of sequence b are pre[b] .. pre[b+1]-1, split-major).
+//
+// Items are taken round-robin by the `gridDim.x` persistent work-groups, so a
+// split of t tiles finishes in about ceil(items / slots) * (t + overhead).
+// Thread c evaluates "split the longest sequence c+1 ways" and the cheapest
+// candidate wins (ties go to the larger split, i.e. fewer partials).  With
+// equal lengths this finds the exact balance; with ragged lengths it keeps
+// the heaviest slot close to the mean.
 template <int NW>
-__device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out) {
+__device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out, int quantum, int UB) {
   const int T = NW * 64;
-  long long total = 0;
+  // quantum: every wave sharing a unit gets the same number of tiles
+  constexpr int kItemOverhead = 8;   // per-item fixed cost, in tiles
+  // lengths (in tiles) into pre[] temporarily, and the longest
   int mx = 0;
   for (int b = threadIdx.x; b < a.B; b += T) {
-    int t = seq_tiles(a, b);
-    total += t;
+    const int t = seq_tiles(a, b);
+    pre[b] = t;
     mx = max(mx, t);
   }
-  block_sum_max<NW>(total, mx, red);
-  const int slots = gridDim.x;
-  const int quantum = NW;      // every wave of the group gets the same number of tiles
+  long long dummy = 0;
+  block_sum_max<NW>(dummy, mx, red);
   int tps;
   if (a.tps_force > 0) {
     tps = a.tps_force;
   } else {
-    long long per_slot = (total * a.U + slots - 1) / slots;
-    tps = (mx <= per_slot) ? mx : (int)((per_slot + 3) / 4);
+    // candidate c = threadIdx.x / 8 + 1 splits of the longest sequence; the 8
+    // threads of a candidate sum the item counts of every 8th sequence
+    static_assert(NW * 64 >= 8, "need at least 8 threads");
+    const int c = threadIdx.x / 8 + 1, j = threadIdx.x & 7;
+    int t = (mx + c - 1) / c;
+    t = max(t, kTpsMin);
+    t = (t + quantum - 1) / quantum * quantum;
+    long long items = 0;
+    for (int b = j; b < a.B; b += 8) items += (pre[b] + t - 1) / t;
+    items += __shfl_xor(items, 1);
+    items += __shfl_xor(items, 2);
+    items += __shfl_xor(items, 4);
+    items *= UB;
+    constexpr long long kInf = (1LL << 36) - 1;
+    long long cost = (items + gridDim.x - 1) / gridDim.x * (long long)(t + kItemOverhead);
+    if (items > a.max_items || cost > kInf) cost = kInf;
+    // arg-min over the block of (cost, -t): ties prefer the larger split
+    unsigned long long k = ((unsigned long long)cost << 27) | (unsigned long long)(0x7ffffff - t);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const unsigned long long y = __shfl_xor(k, o);
+      k = y < k ? y : k;
+    }
+    __syncthreads();
+    unsigned long long* red64 = (unsigned long long*)red;   // NW 8-byte slots (red is 8-byte aligned)
+    if ((threadIdx.x & 63) == 0) red64[threadIdx.x >> 6] = k;
+    __syncthreads();
+    unsigned long long best = red64[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) best = red64[w] < best ? red64[w] : best;
+    tps = 0x7ffffff - (int)(best & 0x7ffffffULL);
   }
   tps = max(tps, kTpsMin);
   tps = (tps + quantum - 1) / quantum * quantum;
   // Grow the split until the partial workspace can hold every item.
   for (int guard = 0; guard < 32; ++guard) {
     long long items = 0;
-    for (int b = threadIdx.x; b < a.B; b += T)
-      items += (long long)((seq_tiles(a, b) + tps - 1) / tps) * a.U;
-    int dummy = 0;
-    block_sum_max<NW>(items, dummy, red);
+    for (int b = threadIdx.x; b < a.B; b += T) items += (long long)((pre[b] + tps - 1) / tps) * UB;
+    int dm = 0;
+    block_sum_max<NW>(items, dm, red);
     if (items <= a.max_items) break;
     tps = min(tps * 2, 1 << 28);
   }
-  block_scan<NW>(a, tps, pre, red);
+  __syncthreads();
+  block_scan<NW>(a, tps, pre, red, UB);
   tps_out = tps;
   return pre[a.B];
 }
@@ -214,8 +252,8 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, const TilePtr& t,
   }
   if constexpr (C::kInt8) {
     if (FULL && std::is_same<ST, F32>::value && a.scale_vec) {
-      const f32x4 k4 = *(const f32x4*)(t.ks + o.ks);
-      const f32x4 v4 = *(const f32x4*)(t.vs + o.vs);
+      const f32x4 k4 = __builtin_nontemporal_load((const f32x4*)(t.ks + o.ks));
+      const f32x4 v4 = __builtin_nontemporal_load((const f32x4*)(t.vs + o.vs));
 #pragma unroll
       for (int i = 0; i < 4; ++i) { c.ks[i] = k4[i]; c.vs[i] = v4[i]; }
     } else {
@@ -407,8 +445,32 @@ __device__ __forceinline__ float load_q(const DecodeArgs& a, int b, int hq, bool
   return mul;
 }
 
+// Waves per SIMD each instantiation is compiled for (its VGPR budget).  A
+// work-group is NW = 8 waves, so below 4 waves per SIMD a CU holds one group.
+template <int D, class KV>
+struct DecodeWaves {
+  static constexpr int value = D <= 64 ? 4 : (D <= 128 ? 2 : 1);
+};
+
+// Geometry of one item inside a work-group of NW waves (all uniform).
+//   U >= NW: the item covers NW units (one per wave), phases P = 1.
+//   U <  NW: the item covers all U units; P = NW / U waves share a unit and
+//            split its tiles by phase (merged through LDS afterwards).
+struct ItemShape {
+  int units;   // units covered by one item (<= NW)
+  int P;       // waves per unit
+};
+template <int NW>
+__device__ __forceinline__ ItemShape item_shape(int U) {
+  ItemShape sh;
+  if (U >= NW) { sh.units = NW; sh.P = 1; }
+  else { sh.units = U; sh.P = NW / U; }
+  return sh;
+}
+
 template <int D, class KV, class QT, class ST, int NW>
-__global__ __launch_bounds__(NW * 64) void decode_main(const DecodeArgs a) {
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DecodeWaves<D, KV>::value)))
+void decode_main(const DecodeArgs a) {
   constexpr int E = D / 16;
   constexpr int KSTEPS = D / 32;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -419,11 +481,12 @@ __global__ __launch_bounds__(NW * 64) void decode_main(const DecodeArgs a) {
   int* red = (int*)(l_l + NW * a.G16);
   int* pre = red + 2 * NW + 2;
 
+  const ItemShape shape = item_shape<NW>(a.U);
   int tps;
-  const int total = plan_items<NW>(a, pre, red, tps);
+  const int total = plan_items<NW>(a, pre, red, tps, shape.P, a.UB);
   if (blockIdx.x == 0) {
     for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[4 + i] = pre[i];
-    if (threadIdx.x == 0) { a.ws_plan[0] = tps; a.ws_plan[1] = total; a.ws_plan[2] = a.U; }
+    if (threadIdx.x == 0) { a.ws_plan[0] = tps; a.ws_plan[1] = total; a.ws_plan[2] = a.UB; }
   }
 
   const int lane = threadIdx.x & 63;
@@ -436,164 +499,209 @@ __global__ __launch_bounds__(NW * 64) void decode_main(const DecodeArgs a) {
   for (int i = 0; i < 4; ++i) lo.v[i] = (uint32_t)((4 * grp + i) * a.v_sn) + (uint32_t)(lane16 * TileT::VB);
   lo.ks = (uint32_t)(4 * grp * a.ks_sn);
   lo.vs = (uint32_t)(4 * grp * a.vs_sn);
+  const int uin = wave / shape.P;        // unit slot of this wave inside an item
+  const int phase = wave - uin * shape.P;
 
   for (int item = blockIdx.x; item < total; item += gridDim.x) {
-    // item -> (b, split, unit): b is the largest index with pre[b] <= item
+    // item -> (b, split, unit block): b is the largest index with pre[b] <= item
     int blo = 0, bhi = a.B;
     while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= item) blo = mid; else bhi = mid; }
     const int b = uniform(blo);
     const int rem = uniform(item - pre[b]);
-    const int split = rem / a.U, unit = rem - split * a.U;
+    const int split = rem / a.UB, ublk = rem - split * a.UB;
+    const int unit = ublk * shape.units + uin;
+    const bool wave_live = uin < shape.units && unit < a.U;
     const int hkv = unit / a.HG, hg = unit - hkv * a.HG;
     const int ntok = uniform(seq_tokens(a, b));
     const int ntile = (ntok + kTile - 1) / kTile;
     const int nsplit = (ntile + tps - 1) / tps;
     const int t_lo = split * tps;
     const int t_hi = min(t_lo + tps, ntile);
-    const int nh = min(16, a.G - 16 * hg);    // live head columns in this unit
+    const int nh = wave_live ? min(16, a.G - 16 * hg) : 0;    // live head columns of this wave's unit
     const bool live = lane16 < nh;
-    const int hq = hkv * a.G + 16 * hg + (live ? lane16 : 0);
-
-    u32x4 qop[KSTEPS], qop_lo[KSTEPS];
-    const float qmul = load_q<D, KV, QT>(a, b, hq, live, grp, qop, qop_lo);
+    const int hq = live ? hkv * a.G + 16 * hg + lane16 : 0;
 
     WaveState<D> st;
     st.m = -INFINITY; st.l = 0.f; st.sexp = -100;
 #pragma unroll
     for (int e = 0; e < E; ++e) st.acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Wave w takes tiles t_lo + w, + NW, ...: `nfull` full tiles (double-
-    // buffered) and possibly the sequence's partial last tile.
-    const bool paged = a.bt != nullptr;
-    const int t_first = t_lo + wave;
-    const int t_full = min(t_hi, ntok / kTile);
-    const int nfull = t_first < t_full ? (t_full - t_first + NW - 1) / NW : 0;
-    const int nt = t_first < t_hi ? (t_hi - t_first + NW - 1) / NW : 0;
-    const int64_t rowk = paged ? 0 : (int64_t)b * a.k_s0, rowv = paged ? 0 : (int64_t)b * a.v_s0;
-    const int64_t rowks = paged ? 0 : (int64_t)b * a.ks_s0, rowvs = paged ? 0 : (int64_t)b * a.vs_s0;
-    const char* kb = a.k + rowk + (int64_t)hkv * a.k_sh;
-    const char* vb = a.v + rowv + (int64_t)hkv * a.v_sh;
-    const char* ksb = a.ks + rowks + (int64_t)hkv * a.ks_sh;
-    const char* vsb = a.vs + rowvs + (int64_t)hkv * a.vs_sh;
-    const int tpp_mask = (1 << a.lg_tiles_per_page) - 1;
-    // tile k of this wave (k uniform) -> base pointers; `pg` holds the page ids
-    // of tiles [w0, w0+64) in lanes 0..63.
-    auto tile_ptr = [&](int t, int phys) {
-      TilePtr tp;
-      int64_t ok, ov, oks, ovs;
-      if (paged) {
-        const int off = (t & tpp_mask) * kTile;
-        ok = (int64_t)phys * a.k_s0 + off * a.k_sn;
-        ov = (int64_t)phys * a.v_s0 + off * a.v_sn;
-        oks = (int64_t)phys * a.ks_s0 + off * a.ks_sn;
-        ovs = (int64_t)phys * a.vs_s0 + off * a.vs_sn;
-      } else {
-        ok = (int64_t)t * kTile * a.k_sn;
-        ov = (int64_t)t * kTile * a.v_sn;
-        oks = (int64_t)t * kTile * a.ks_sn;
-        ovs = (int64_t)t * kTile * a.vs_sn;
+    if (wave_live) {
+      u32x4 qop[KSTEPS], qop_lo[KSTEPS];
+      const float qmul = load_q<D, KV, QT>(a, b, hq, live, grp, qop, qop_lo);
+
+      // This wave takes tiles t_lo + phase, + P, ...: `nfull` full tiles
+      // (double-buffered) and possibly the sequence's partial last tile.
+      const int P = shape.P;
+      const bool paged = a.bt != nullptr;
+      const int t_first = t_lo + phase;
+      const int t_full = min(t_hi, ntok / kTile);
+      const int nfull = t_first < t_full ? (t_full - t_first + P - 1) / P : 0;
+      const int nt = t_first < t_hi ? (t_hi - t_first + P - 1) / P : 0;
+      const int64_t rowk = paged ? 0 : (int64_t)b * a.k_s0, rowv = paged ? 0 : (int64_t)b * a.v_s0;
+      const int64_t rowks = paged ? 0 : (int64_t)b * a.ks_s0, rowvs = paged ? 0 : (int64_t)b * a.vs_s0;
+      const char* kb = a.k + rowk + (int64_t)hkv * a.k_sh;
+      const char* vb = a.v + rowv + (int64_t)hkv * a.v_sh;
+      const char* ksb = a.ks + rowks + (int64_t)hkv * a.ks_sh;
+      const char* vsb = a.vs + rowvs + (int64_t)hkv * a.vs_sh;
+      const int tpp_mask = (1 << a.lg_tiles_per_page) - 1;
+      auto tile_ptr = [&](int t, int phys) {
+        TilePtr tp;
+        int64_t ok, ov, oks, ovs;
+        if (paged) {
+          const int off = (t & tpp_mask) * kTile;
+          ok = (int64_t)phys * a.k_s0 + off * a.k_sn;
+          ov = (int64_t)phys * a.v_s0 + off * a.v_sn;
+          oks = (int64_t)phys * a.ks_s0 + off * a.ks_sn;
+          ovs = (int64_t)phys * a.vs_s0 + off * a.vs_sn;
+        } else {
+          ok = (int64_t)t * kTile * a.k_sn;
+          ov = (int64_t)t * kTile * a.v_sn;
+          oks = (int64_t)t * kTile * a.ks_sn;
+          ovs = (int64_t)t * kTile * a.vs_sn;
+        }
+        tp.k = kb + ok; tp.v = vb + ov; tp.ks = ksb + oks; tp.vs = vsb + ovs;
+        return tp;
+      };
+      // page ids of this wave's tiles [w0, w0 + 64) in lanes 0..63
+      auto page_ids = [&](int w0, int wn) {
+        int pg = 0;
+        if (paged && lane < wn) {
+          const int t = t_first + (w0 + lane) * P;
+          pg = a.bt[(int64_t)b * a.bt_sb + (int64_t)(t >> a.lg_tiles_per_page) * a.bt_sl];
+          pg = ((unsigned)pg < (unsigned long long)a.num_pages) ? pg : 0;   // never read outside the pool
+        }
+        return pg;
+      };
+      TileT bufA, bufB;
+      for (int w0 = 0; w0 < nfull; w0 += 64) {
+        const int wn = min(64, nfull - w0);
+        const int pg = page_ids(w0, wn);
+        int k = 0;
+        load_tile<D, KV, ST, true>(a, tile_ptr(t_first + w0 * P, __builtin_amdgcn_readlane(pg, 0)), lo, 16,
+                                   bufA, lane16, grp);
+        while (true) {
+          if (k + 1 < wn)
+            load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * P, __builtin_amdgcn_readlane(pg, k + 1)),
+                                       lo, 16, bufB, lane16, grp);
+          compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, 0, ntok, grp, st);
+          if (++k >= wn) break;
+          if (k + 1 < wn)
+            load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * P, __builtin_amdgcn_readlane(pg, k + 1)),
+                                       lo, 16, bufA, lane16, grp);
+          compute_tile<D, KV, QT, ST, true>(bufB, qop, qop_lo, qmul, 0, ntok, grp, st);
+          if (++k >= wn) break;
+        }
       }
-      tp.k = kb + ok; tp.v = vb + ov; tp.ks = ksb + oks; tp.vs = vsb + ovs;
-      return tp;
-    };
-    auto page_ids = [&](int w0, int wn) {
-      int pg = 0;
-      if (paged && lane < wn) {
-        const int t = t_first + (w0 + lane) * NW;
-        pg = a.bt[(int64_t)b * a.bt_sb + (int64_t)(t >> a.lg_tiles_per_page) * a.bt_sl];
-        pg = ((unsigned)pg < (unsigned long long)a.num_pages) ? pg : 0;   // never read outside the pool
+      if (nt > nfull) {  // the sequence's partial last tile belongs to this wave
+        const int t = t_first + nfull * P;
+        const int pg = page_ids(nfull, 1);
+        load_tile<D, KV, ST, false>(a, tile_ptr(t, __builtin_amdgcn_readlane(pg, 0)), lo, ntok - t * kTile,
+                                    bufA, lane16, grp);
+        compute_tile<D, KV, QT, ST, false>(bufA, qop, qop_lo, qmul, t, ntok, grp, st);
       }
-      return pg;
-    };
-    Tile<D, KV, ST> bufA, bufB;
-    for (int w0 = 0; w0 < nfull; w0 += 64) {
-      const int wn = min(64, nfull - w0);
-      const int pg = page_ids(w0, wn);
-      int k = 0;
-      load_tile<D, KV, ST, true>(a, tile_ptr(t_first + w0 * NW, __builtin_amdgcn_readlane(pg, 0)), lo, 16,
-                                 bufA, lane16, grp);
-      while (true) {
-        if (k + 1 < wn)
-          load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * NW, __builtin_amdgcn_readlane(pg, k + 1)),
-                                     lo, 16, bufB, lane16, grp);
-        compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, 0, ntok, grp, st);
-        if (++k >= wn) break;
-        if (k + 1 < wn)
-          load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * NW, __builtin_amdgcn_readlane(pg, k + 1)),
-                                     lo, 16, bufA, lane16, grp);
-        compute_tile<D, KV, QT, ST, true>(bufB, qop, qop_lo, qmul, 0, ntok, grp, st);
-        if (++k >= wn) break;
-      }
-    }
-    if (nt > nfull) {  // the sequence's partial last tile belongs to this wave
-      const int t = t_first + nfull * NW;
-      const int pg = page_ids(nfull, 1);
-      load_tile<D, KV, ST, false>(a, tile_ptr(t, __builtin_amdgcn_readlane(pg, 0)), lo, ntok - t * kTile,
-                                  bufA, lane16, grp);
-      compute_tile<D, KV, QT, ST, false>(bufA, qop, qop_lo, qmul, t, ntok, grp, st);
     }
 
-    // ---- merge the NW waves through LDS
     const float lsum = wave_sum_xor16_32(st.l);
     const float unscale = std::is_same<KV, I8>::value ? ldexpf(1.0f, st.sexp - 4) : 1.0f;
-    if (live) {
-      float* dst = l_acc + (wave * a.G16 + lane16) * D + grp * (D / 4);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int e = 0; e < E; ++e) dst[i * E + e] = st.acc[e][i] * unscale;
-      if (grp == 0) { l_m[wave * a.G16 + lane16] = st.m; l_l[wave * a.G16 + lane16] = lsum; }
-    }
-    __syncthreads();
     const bool direct = nsplit == 1;
-    for (int idx = threadIdx.x; idx < nh * D; idx += NW * 64) {
-      const int cc = idx / D, d = idx - cc * D;
-      float M = -INFINITY;
+    // partial slot of (item, unit slot, head col)
+    const int64_t pslot = ((int64_t)item * NW + uin) * a.G16;
+    if (shape.P == 1) {
+      // one wave owns each unit: write straight from registers
+      if (live) {
+        if (direct) {
+          const float inv = unscale / (lsum == 0.f ? 1.f : lsum);
+          char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + grp * (D / 4) * 2;
 #pragma unroll
-      for (int w = 0; w < NW; ++w) M = fmaxf(M, l_m[w * a.G16 + cc]);
-      float L = 0.f, A = 0.f;
-      if (M != -INFINITY) {
+          for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-          const float mw = l_m[w * a.G16 + cc];
-          const float wt = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-          L += wt * l_l[w * a.G16 + cc];
-          A += wt * l_acc[(w * a.G16 + cc) * D + d];
+            for (int e = 0; e < E; e += 2) {
+              const uint32_t w = pack2(QT{}, st.acc[e][i] * inv, st.acc[e + 1][i] * inv);
+              *(uint32_t*)(op + (i * E + e) * 2) = w;
+            }
+        } else {
+          float* dst = a.ws_acc + (pslot + lane16) * D + grp * (D / 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int e = 0; e < E; e += 4)
+              *(f32x4*)(dst + i * E + e) = f32x4{st.acc[e][i] * unscale, st.acc[e + 1][i] * unscale,
+                                                 st.acc[e + 2][i] * unscale, st.acc[e + 3][i] * unscale};
+          if (grp == 0) {
+            a.ws_ml[(pslot + lane16) * 2 + 0] = st.m;
+            a.ws_ml[(pslot + lane16) * 2 + 1] = lsum;
+          }
         }
       }
-      const int hqo = hkv * a.G + 16 * hg + cc;
-      if (direct) {
-        char* op = a.out + b * a.o_sb + (int64_t)hqo * a.o_sh + d * (int)sizeof(uint16_t);
-        store_out(QT{}, op, A / (L == 0.f ? 1.f : L));
-      } else {
-        a.ws_acc[((int64_t)item * a.G16 + cc) * D + d] = A;
-        if (d == 0) {
-          a.ws_ml[((int64_t)item * a.G16 + cc) * 2 + 0] = M;
-          a.ws_ml[((int64_t)item * a.G16 + cc) * 2 + 1] = L;
+    } else {
+      // P waves per unit: merge their (m, l, acc) through LDS
+      if (live) {
+        float* dst = l_acc + (wave * a.G16 + lane16) * D + grp * (D / 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int e = 0; e < E; ++e) dst[i * E + e] = st.acc[e][i] * unscale;
+      }
+      if (lane16 < a.G16 && grp == 0) {
+        l_m[wave * a.G16 + lane16] = live ? st.m : -INFINITY;
+        l_l[wave * a.G16 + lane16] = live ? lsum : 0.f;
+      }
+      __syncthreads();
+      const int nh_all = min(16, a.G);                 // head columns per unit (same for every unit here)
+      for (int idx = threadIdx.x; idx < shape.units * nh_all * D; idx += NW * 64) {
+        const int us = idx / (nh_all * D);
+        const int r2 = idx - us * nh_all * D;
+        const int cc = r2 / D, d = r2 - cc * D;
+        const int u2 = ublk * shape.units + us;
+        const int hkv2 = u2 / a.HG, hg2 = u2 - hkv2 * a.HG;
+        if (16 * hg2 + cc >= a.G) continue;
+        float M = -INFINITY;
+        for (int p2 = 0; p2 < shape.P; ++p2) M = fmaxf(M, l_m[(us * shape.P + p2) * a.G16 + cc]);
+        float L = 0.f, A = 0.f;
+        if (M != -INFINITY) {
+          for (int p2 = 0; p2 < shape.P; ++p2) {
+            const int w2 = us * shape.P + p2;
+            const float mw = l_m[w2 * a.G16 + cc];
+            const float wt = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
+            L += wt * l_l[w2 * a.G16 + cc];
+            A += wt * l_acc[(w2 * a.G16 + cc) * D + d];
+          }
+        }
+        const int hqo = hkv2 * a.G + 16 * hg2 + cc;
+        if (direct) {
+          char* op = a.out + b * a.o_sb + (int64_t)hqo * a.o_sh + d * (int)sizeof(uint16_t);
+          store_out(QT{}, op, A / (L == 0.f ? 1.f : L));
+        } else {
+          const int64_t ps = ((int64_t)item * NW + us) * a.G16 + cc;
+          a.ws_acc[ps * D + d] = A;
+          if (d == 0) { a.ws_ml[ps * 2 + 0] = M; a.ws_ml[ps * 2 + 1] = L; }
         }
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
 // Merge split-K partials of one (sequence, query head) per wave; writes zeros
 // for empty sequences and skips sequences the main kernel wrote directly.
-template <int D, class OT>
+template <int D, class OT, int NW>
 __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= a.B * a.Hq) return;
   const int b = row / a.Hq, hq = row - b * a.Hq;
   const int p0 = a.ws_plan[4 + b], p1 = a.ws_plan[4 + b + 1];
-  const int nsplit = (p1 - p0) / a.U;
+  const int nsplit = (p1 - p0) / a.UB;
   if (nsplit == 1) return;
   const int hkv = hq / a.G, gi = hq - hkv * a.G, hg = gi >> 4, cc = gi & 15;
   const int unit = hkv * a.HG + hg;
+  const ItemShape shape = item_shape<NW>(a.U);
+  const int ublk = unit / shape.units, uin = unit - ublk * shape.units;
   char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh;
+  auto slot = [&](int s) { return ((int64_t)(p0 + s * a.UB + ublk) * NW + uin) * a.G16 + cc; };
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s)
-    M = fmaxf(M, a.ws_ml[((int64_t)(p0 + s * a.U + unit) * a.G16 + cc) * 2]);
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_ml[slot(s) * 2]);
   constexpr int PER = (D + 63) / 64;
   float A[PER];
 #pragma unroll
@@ -601,7 +709,7 @@ __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
   float L = 0.f;
   if (M != -INFINITY) {
     for (int s = 0; s < nsplit; ++s) {
-      const int64_t it = (int64_t)(p0 + s * a.U + unit) * a.G16 + cc;
+      const int64_t it = slot(s);
       const float mw = a.ws_ml[it * 2];
       if (mw == -INFINITY) continue;
       const float wt = fast_exp2(mw - M);

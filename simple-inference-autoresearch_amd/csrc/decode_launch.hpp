@@ -8,7 +8,7 @@
 
 namespace sia {
 
-constexpr int kDecodeWaves = 4;   // waves per work-group
+constexpr int kDecodeWaves = 8;   // waves per work-group: one per KV-head unit of a page
 
 struct DecodeLaunch {
   DecodeArgs a;
@@ -41,18 +41,23 @@ int launch_decode_typed(DecodeLaunch& L) {
   if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
   const int rows = L.a.B * L.a.Hq;
-  hipLaunchKernelGGL((decode_reduce<D, QT>), dim3((rows + 3) / 4), dim3(256), 0, L.stream, L.a);
+  hipLaunchKernelGGL((decode_reduce<D, QT, NW>), dim3((rows + 3) / 4), dim3(256), 0, L.stream, L.a);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode reduce launch: %s", hipGetErrorString(e));
   return SIA_OK;
 }
+
+// head_dim 256 is compiled in its own unit (decode_d256.hip) with different
+// register-allocation flags.
+template <class KV, class QT, class ST>
+int launch_decode_256(DecodeLaunch& L);
 
 template <class KV, class QT, class ST>
 int launch_decode_d(DecodeLaunch& L) {
   switch (L.D) {
     case 64: return launch_decode_typed<64, KV, QT, ST>(L);
     case 128: return launch_decode_typed<128, KV, QT, ST>(L);
-    case 256: return launch_decode_typed<256, KV, QT, ST>(L);
+    case 256: return launch_decode_256<KV, QT, ST>(L);
     default: return fail(SIA_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", L.D);
   }
 }
