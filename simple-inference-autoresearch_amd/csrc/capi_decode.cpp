@@ -13,7 +13,6 @@ using namespace sia;
 
 namespace {
 
-constexpr int kPlanHeader = 4;
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 

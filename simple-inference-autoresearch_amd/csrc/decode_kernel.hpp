@@ -39,6 +39,9 @@
 namespace sia {
 
 constexpr int kTile = 16;          // tokens per MFMA tile
+// Plan header in the workspace (ints): split size, item count, unit blocks per
+// (sequence, split), the work counter; the item prefix per sequence follows.
+constexpr int kPlanTps = 0, kPlanTotal = 1, kPlanUB = 2, kPlanCounter = 3, kPlanHeader = 4;
 constexpr int kTpsMin = 8;         // smallest split, in tiles
 // The running max is only raised when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^8: well inside f16/bf16 range, and the
@@ -61,6 +64,7 @@ struct DecodeArgs {
   float qk_scale;                                    // sm_scale * log2(e)
   float* ws_acc; float* ws_ml; int32_t* ws_plan; int32_t max_items; int32_t G16;
   int32_t tps_force;
+  int32_t slots;                                     // persistent work-groups of decode_main
   int32_t scale_vec;                                 // scale rows allow 16-byte vector loads
 };
 
@@ -140,7 +144,7 @@ __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pr
 // equal lengths this finds the exact balance; with ragged lengths it keeps
 // the heaviest slot close to the mean.
 template <int NW>
-__device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out, int quantum, int UB) {
+__device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out, int quantum, int UB, int slots) {
   const int T = NW * 64;
   // quantum: every wave sharing a unit gets the same number of tiles
   constexpr int kItemOverhead = 8;   // per-item fixed cost, in tiles
@@ -171,7 +175,7 @@ __device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out,
     items += __shfl_xor(items, 4);
     items *= UB;
     constexpr long long kInf = (1LL << 36) - 1;
-    long long cost = (items + gridDim.x - 1) / gridDim.x * (long long)(t + kItemOverhead);
+    long long cost = (items + slots - 1) / slots * (long long)(t + kItemOverhead);
     if (items > a.max_items || cost > kInf) cost = kInf;
     // arg-min over the block of (cost, -t): ties prefer the larger split
     unsigned long long k = ((unsigned long long)cost << 27) | (unsigned long long)(0x7ffffff - t);
@@ -482,12 +486,20 @@ void decode_main(const DecodeArgs a) {
   int* pre = red + 2 * NW + 2;
 
   const ItemShape shape = item_shape<NW>(a.U);
-  int tps;
-  const int total = plan_items<NW>(a, pre, red, tps, shape.P, a.UB);
-  if (blockIdx.x == 0) {
-    for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[4 + i] = pre[i];
-    if (threadIdx.x == 0) { a.ws_plan[0] = tps; a.ws_plan[1] = total; a.ws_plan[2] = a.UB; }
-  }
+  // the plan (written by decode_plan just before this kernel): split size,
+  // item count and the item prefix per sequence
+  const int tps = uniform(a.ws_plan[kPlanTps]);
+  const int total = uniform(a.ws_plan[kPlanTotal]);
+  for (int i = threadIdx.x; i <= a.B; i += NW * 64) pre[i] = a.ws_plan[kPlanHeader + i];
+  // Work assignment: group g first takes item g; items past the grid are
+  // handed out by an atomic counter (zeroed by decode_plan), so a group that
+  // finishes early takes more and ragged batches stay balanced.  Only those
+  // late, naturally staggered requests touch the counter: a burst of
+  // same-address atomics from every group at launch costs more than it saves.
+  int* l_item = red;   // LDS slot broadcasting the next item
+  const bool steal = total > (int)gridDim.x;
+  __syncthreads();
+  int next_item = blockIdx.x;
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -502,7 +514,11 @@ void decode_main(const DecodeArgs a) {
   const int uin = wave / shape.P;        // unit slot of this wave inside an item
   const int phase = wave - uin * shape.P;
 
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+  while (next_item < total) {
+    const int item = uniform(next_item);
+    // request the following item now; its index is only needed at the end
+    int stolen = 0;
+    if (steal && threadIdx.x == 0) stolen = (int)gridDim.x + atomicAdd(&a.ws_plan[kPlanCounter], 1);
     // item -> (b, split, unit block): b is the largest index with pre[b] <= item
     int blo = 0, bhi = a.B;
     while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= item) blo = mid; else bhi = mid; }
@@ -678,8 +694,35 @@ void decode_main(const DecodeArgs a) {
           if (d == 0) { a.ws_ml[ps * 2 + 0] = M; a.ws_ml[ps * 2 + 1] = L; }
         }
       }
-      __syncthreads();
     }
+    if (steal) {
+      if (threadIdx.x == 0) l_item[0] = stolen;
+      __syncthreads();
+      next_item = l_item[0];
+      __syncthreads();   // l_item and the merge LDS are free for the next item
+    } else {
+      if (shape.P > 1) __syncthreads();   // merge LDS free for reuse
+      next_item += gridDim.x;
+    }
+  }
+}
+
+// One work-group: decide the split from the device-side lengths, write the
+// item prefix and zero the work counter for decode_main.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void decode_plan(const DecodeArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int* red = (int*)smem;            // 2*NW+2 ints (8-byte aligned)
+  int* pre = red + 2 * NW + 2;      // B+1 ints
+  const ItemShape shape = item_shape<NW>(a.U);
+  int tps;
+  const int total = plan_items<NW>(a, pre, red, tps, shape.P, a.UB, a.slots);
+  for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[kPlanHeader + i] = pre[i];
+  if (threadIdx.x == 0) {
+    a.ws_plan[kPlanTps] = tps;
+    a.ws_plan[kPlanTotal] = total;
+    a.ws_plan[kPlanUB] = a.UB;
+    a.ws_plan[kPlanCounter] = 0;
   }
 }
 
@@ -691,7 +734,7 @@ __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   if (row >= a.B * a.Hq) return;
   const int b = row / a.Hq, hq = row - b * a.Hq;
-  const int p0 = a.ws_plan[4 + b], p1 = a.ws_plan[4 + b + 1];
+  const int p0 = a.ws_plan[kPlanHeader + b], p1 = a.ws_plan[kPlanHeader + b + 1];
   const int nsplit = (p1 - p0) / a.UB;
   if (nsplit == 1) return;
   const int hkv = hq / a.G, gi = hq - hkv * a.G, hg = gi >> 4, cc = gi & 15;
@@ -700,24 +743,42 @@ __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
   const int ublk = unit / shape.units, uin = unit - ublk * shape.units;
   char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh;
   auto slot = [&](int s) { return ((int64_t)(p0 + s * a.UB + ublk) * NW + uin) * a.G16 + cc; };
+  // (m, l) of up to 64 splits per pass, one split per lane
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.ws_ml[slot(s) * 2]);
+  for (int s0 = 0; s0 < nsplit; s0 += 64) {
+    const int s = s0 + lane;
+    const float m = s < nsplit ? a.ws_ml[slot(s) * 2] : -INFINITY;
+    M = fmaxf(M, m);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
   constexpr int PER = (D + 63) / 64;
   float A[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) A[i] = 0.f;
   float L = 0.f;
   if (M != -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
-      const int64_t it = slot(s);
-      const float mw = a.ws_ml[it * 2];
-      if (mw == -INFINITY) continue;
-      const float wt = fast_exp2(mw - M);
-      L += wt * a.ws_ml[it * 2 + 1];
+    for (int s0 = 0; s0 < nsplit; s0 += 64) {
+      const int s = s0 + lane;
+      float wt = 0.f, lw = 0.f;
+      if (s < nsplit) {
+        const float m = a.ws_ml[slot(s) * 2];
+        wt = m == -INFINITY ? 0.f : fast_exp2(m - M);
+        lw = wt * a.ws_ml[slot(s) * 2 + 1];
+      }
 #pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int d = lane + 64 * i;
-        if (d < D) A[i] += wt * a.ws_acc[it * D + d];
+      for (int o = 32; o > 0; o >>= 1) lw += __shfl_xor(lw, o);
+      L += lw;
+      const int n = min(64, nsplit - s0);
+#pragma unroll 4
+      for (int j = 0; j < n; ++j) {
+        const float w = __shfl(wt, j);
+        const float* src = a.ws_acc + slot(s0 + j) * D;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int d = lane + 64 * i;
+          if (d < D) A[i] += w * src[d];
+        }
       }
     }
   }

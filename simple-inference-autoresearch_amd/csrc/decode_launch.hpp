@@ -30,13 +30,17 @@ int launch_decode_typed(DecodeLaunch& L) {
   constexpr int NW = kDecodeWaves;
   auto kmain = decode_main<D, KV, QT, ST, NW>;
   const size_t lds = decode_lds_bytes(D, L.a.G16, L.a.B, NW);
-  int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
+  const int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
   if (occ <= 0) return fail(SIA_ERR_LAUNCH, "decode kernel does not fit on a CU (LDS %zu B)", lds);
-  const int slots = device_info().cus * occ;
+  L.a.slots = device_info().cus * occ;
+  // 1. plan (one work-group), 2. main (persistent, work stealing), 3. split-K merge
+  hipLaunchKernelGGL((decode_plan<NW>), dim3(1), dim3(NW * 64), (size_t)(2 * NW + 2 + L.a.B + 1) * 4, L.stream, L.a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode plan launch: %s", hipGetErrorString(e));
   if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
-  hipLaunchKernelGGL(kmain, dim3(slots), dim3(NW * 64), lds, L.stream, L.a);
-  hipError_t e = hipGetLastError();
+  hipLaunchKernelGGL(kmain, dim3(L.a.slots), dim3(NW * 64), lds, L.stream, L.a);
+  e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode launch: %s", hipGetErrorString(e));
   if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
