@@ -162,6 +162,30 @@ def bench_decode_config(pkg, case, steps, warmup):
     }
 
 
+def bench_prefill_config(pkg, steps: int, warmup: int):
+    """Config 4: causal bf16 prefill B4 T2048 32/8 heads D128 -> MFMA TFLOP/s (T^2/2 FLOP convention)."""
+    import torch
+
+    syn = _syn()
+    q, k, v = syn.cfg4(torch.device("cuda:0"))
+    B, Hq, T, D = q.shape
+    for _ in range(warmup):
+        pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = syn.prefill_flops(B, Hq, T, D)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 1), "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "algorithmic_flops": flops, "workload": "config 4: causal prefill bf16 B4 T2048 32/8 heads D128"}
+
+
 def load_traffic(kernel: str):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), or None."""
     path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.json")
@@ -179,7 +203,7 @@ def main(argv=None):
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-others", action="store_true", help="skip configs 2, 4 and 5")
-    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg5"],
+    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5"],
                    help="decode config to run as the headline (profiling runs)")
     args = p.parse_args(argv)
 
@@ -197,6 +221,11 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.config == "cfg4":   # prefill only (profiling runs)
+        r = bench_prefill_config(pkg, args.steps, args.warmup)
+        print(f"[bench] cfg4: {r}", file=sys.stderr, flush=True)
+        print(json.dumps({"config": "cfg4", **r}), flush=True)
+        return 0
     case = getattr(syn, args.config)(dev)
     torch.cuda.synchronize()
     print(f"[bench] {args.config}: inputs resident ({syn.decode_bytes(case)/1e9:.3f} GB algorithmic)",
@@ -253,6 +282,8 @@ def main(argv=None):
             print(f"[bench] {name}: {others[name]}", file=sys.stderr, flush=True)
             del c
             torch.cuda.empty_cache()
+        others["cfg4"] = bench_prefill_config(pkg, max(20, args.steps // 2), args.warmup)
+        print(f"[bench] cfg4: {others['cfg4']}", file=sys.stderr, flush=True)
         result["other_configs"] = others
         case = None
 

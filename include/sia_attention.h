@@ -131,6 +131,15 @@ int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_poo
                                     void* workspace, size_t workspace_bytes,
                                     const sia_decode_options* opts, void* stream);
 
+/* Replaces attention_flash_triton (kernels/attention_kernel.py:235-305).
+ * q (B,Hq,Tq,D), k,v (B,Hkv,Tk,D): f16|bf16 views, head_dim contiguous,
+ * 16-byte aligned rows; out (B,Hq,Tq,D) view in q's dtype -- a transposed
+ * view of a (B,Tq,Hq,D) buffer gives the reference's out_token_major layout.
+ * causal != 0 applies the bottom-right mask: row i sees keys <= (Tk-Tq)+i;
+ * rows that see no key are written as zeros.  head_dim 64 or 128. */
+int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
+                            float sm_scale, const sia_tensor* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -23,9 +23,11 @@ from .decode import (
     paged_attention_flash_decode,
     paged_gqa_int8_flash_decode,
 )
+from .prefill import attention_flash_triton
 
 __all__ = [
     "LibraryMissing",
+    "attention_flash_triton",
     "SiaError",
     "attention_flash_decode",
     "attention_flash_decode_int8",

@@ -1,0 +1,67 @@
+// extern "C" prefill entry point: validation and dispatch.
+#include <math.h>
+#include <string.h>
+
+#include "host_util.hpp"
+#include "prefill_launch.hpp"
+
+using namespace sia;
+
+namespace {
+
+int check4(const sia_tensor* t, const char* name) {
+  if (t == nullptr || t->data == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "%s is missing", name);
+  if (t->ndim != 4) return fail(SIA_ERR_INVALID_ARGUMENT, "%s must have 4 dims", name);
+  if (t->stride[3] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "%s must be contiguous along head_dim", name);
+  if (!aligned16(t->data)) return fail(SIA_ERR_INVALID_ARGUMENT, "%s must be 16-byte aligned", name);
+  for (int d = 0; d < 3; ++d)
+    if (bstride(t, d) % 16) return fail(SIA_ERR_INVALID_ARGUMENT, "%s strides must be multiples of 16 bytes", name);
+  return SIA_OK;
+}
+
+}  // namespace
+
+extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
+                                       float sm_scale, const sia_tensor* out, void* stream) {
+  int rc;
+  if ((rc = check4(q, "q")) || (rc = check4(k, "k")) || (rc = check4(v, "v")) || (rc = check4(out, "out"))) return rc;
+  if (q->dtype != SIA_F16 && q->dtype != SIA_BF16)
+    return fail(SIA_ERR_UNSUPPORTED, "q dtype %s: expected float16 or bfloat16", dtype_name(q->dtype));
+  if (k->dtype != q->dtype || v->dtype != q->dtype || out->dtype != q->dtype)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "q, k, v and out must share one dtype");
+  const int64_t B = q->shape[0], Hq = q->shape[1], Tq = q->shape[2], D = q->shape[3];
+  const int64_t Hkv = k->shape[1], Tk = k->shape[2];
+  if (k->shape[0] != B || v->shape[0] != B || k->shape[3] != D || v->shape[3] != D || v->shape[1] != Hkv ||
+      v->shape[2] != Tk)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "k and v must be (B, Hkv, Tk, D) matching q");
+  if (out->shape[0] != B || out->shape[1] != Hq || out->shape[2] != Tq || out->shape[3] != D)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "out must be a (B, Hq, Tq, D) view");
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Tq < 0 || Tk < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (Hq % Hkv) return fail(SIA_ERR_INVALID_ARGUMENT, "Hq must be a multiple of Hkv");
+  if (D != 64 && D != 128) return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (64, 128)", (long long)D);
+  if (Tq > (1 << 30) || Tk > (1 << 30)) return fail(SIA_ERR_UNSUPPORTED, "sequence too long");
+  if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return fail(SIA_ERR_INVALID_ARGUMENT, "sm_scale must be positive");
+  const DeviceInfo& dev = device_info();
+  if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
+  if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
+  if (Tq == 0) return SIA_OK;
+
+  PrefillLaunch L;
+  memset(&L, 0, sizeof(L));
+  PrefillArgs& a = L.a;
+  a.q = (const char*)q->data; a.q_sb = bstride(q, 0); a.q_sh = bstride(q, 1); a.q_sm = bstride(q, 2);
+  a.k = (const char*)k->data; a.k_sb = bstride(k, 0); a.k_sh = bstride(k, 1); a.k_sn = bstride(k, 2);
+  a.v = (const char*)v->data; a.v_sb = bstride(v, 0); a.v_sh = bstride(v, 1); a.v_sn = bstride(v, 2);
+  a.out = (char*)out->data; a.o_sb = bstride(out, 0); a.o_sh = bstride(out, 1); a.o_sm = bstride(out, 2);
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.Tq = (int)Tq; a.Tk = (int)Tk;
+  a.causal = causal != 0;
+  a.qk_scale = sm_scale * 1.4426950408889634f;
+  a.nqblk = (int)((Tq + kPfBM - 1) / kPfBM);
+  const int64_t groups = (int64_t)a.nqblk * B * Hkv;   // work-groups come in runs of G sharing a KV head
+  if (groups * a.G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "grid too large");
+  a.remap = groups % 8 == 0;
+  L.D = (int)D;
+  L.dtype = q->dtype;
+  L.stream = (hipStream_t)stream;
+  return launch_prefill(L);
+}

@@ -1,0 +1,26 @@
+// Prefill (flash-attention forward) instantiations and launcher.
+#include "host_util.hpp"
+#include "prefill_kernel.hpp"
+#include "prefill_launch.hpp"
+
+namespace sia {
+
+template <int D, class T>
+static int launch_prefill_typed(PrefillLaunch& L) {
+  const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
+  hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(256), 0, L.stream, L.a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
+  return SIA_OK;
+}
+
+int launch_prefill(PrefillLaunch& L) {
+  const bool bf = L.dtype == SIA_BF16;
+  switch (L.D) {
+    case 64: return bf ? launch_prefill_typed<64, BF16>(L) : launch_prefill_typed<64, F16>(L);
+    case 128: return bf ? launch_prefill_typed<128, BF16>(L) : launch_prefill_typed<128, F16>(L);
+    default: return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %d not supported (64, 128)", L.D);
+  }
+}
+
+}  // namespace sia

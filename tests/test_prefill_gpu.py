@@ -1,0 +1,130 @@
+"""GPU parity of the prefill kernel (attention_flash_triton) against the float64 oracle.
+
+Tolerance: max-abs <= 2e-3 against the oracle, or one unit in the last place
+of the output dtype where |ref| makes a single output rounding larger than
+that (bf16 ulp >= 2e-3 once |o| >= 0.25).  The PV product uses f16 P and V
+(the reference rounds P to the input dtype; bf16 P alone would exceed 2e-3 on
+rows with few keys).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def f64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def ulp(x, dtype):
+    mant = {torch.bfloat16: 7, torch.float16: 10}[dtype]
+    return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -24))) - mant)
+
+
+def check(out, ref, what, atol=2e-3):
+    g = f64(out)
+    assert np.isfinite(g).all(), what
+    err = np.abs(g - ref)
+    allowed = np.maximum(atol, ulp(ref, out.dtype))
+    i = np.unravel_index(np.argmax(err / allowed), err.shape)
+    assert (err <= allowed).all(), (f"{what}: max err {err.max():.3e}; worst at {i}: got {g[i]:.5f} "
+                                    f"ref {ref[i]:.5f} allowed {allowed[i]:.2e}")
+    return float(err.max())
+
+
+def qkv(B, Hq, Hkv, Tq, Tk, D, dtype, seed, scale=0.5):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    q = (torch.randn(B, Hq, Tq, D, generator=g, device=DEV) * scale).to(dtype)
+    k = (torch.randn(B, Hkv, Tk, D, generator=g, device=DEV) * scale).to(dtype)
+    v = (torch.randn(B, Hkv, Tk, D, generator=g, device=DEV) * scale).to(dtype)
+    return q, k, v
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T", [1, 17, 128, 130, 300])
+@pytest.mark.parametrize("causal", [True, False])
+def test_self_attention(gpu_pkg, D, dtype, T, causal):
+    announce(f"prefill D={D} {dtype} T={T} causal={causal}")
+    q, k, v = qkv(2, 8, 2, T, T, D, dtype, seed=T + D)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    check(out, O.flash_attention(f64(q), f64(k), f64(v), causal), f"D={D} T={T}")
+
+
+@pytest.mark.parametrize("Tq,Tk", [(1, 700), (64, 300), (200, 513), (100, 64), (3, 1)])
+def test_offset_causal(gpu_pkg, Tq, Tk):
+    """Chunked prefill (Tq < Tk) and Tq > Tk, where leading rows see nothing."""
+    announce(f"prefill offsets Tq={Tq} Tk={Tk}")
+    q, k, v = qkv(1, 8, 2, Tq, Tk, 128, torch.bfloat16, seed=Tq * 7 + Tk)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    ref = O.flash_attention(f64(q), f64(k), f64(v), True)
+    check(out, ref, f"Tq={Tq} Tk={Tk}")
+    if Tq > Tk:
+        assert torch.all(out[:, :, :Tq - Tk] == 0)
+
+
+def test_strided_views_and_token_major(gpu_pkg):
+    """The model passes transposed (B,T,H,D) views and wants token-major output."""
+    announce("prefill strided views / token-major output")
+    B, T, Hq, Hkv, D = 2, 200, 32, 8, 128
+    g = torch.Generator(device=DEV).manual_seed(3)
+    qt = (torch.randn(B, T, Hq, D, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    kt = (torch.randn(B, T, Hkv, D, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    vt = (torch.randn(B, T, Hkv, D, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    q, k, v = qt.transpose(1, 2), kt.transpose(1, 2), vt.transpose(1, 2)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=True, assume_contiguous=True, out_token_major=True)
+    ref_layout = gpu_pkg.attention_flash_triton(q.contiguous(), k.contiguous(), v.contiguous(), causal=True)
+    torch.cuda.synchronize()
+    assert out.shape == (B, T, Hq, D)
+    assert torch.equal(out.transpose(1, 2), ref_layout)
+    check(ref_layout, O.flash_attention(f64(q), f64(k), f64(v), True), "strided")
+
+
+def test_gqa_mapping(gpu_pkg):
+    """Each query head reads KV head hq // G: give each KV head a constant V."""
+    announce("prefill GQA mapping")
+    B, T, Hq, Hkv, D = 1, 64, 8, 2, 64
+    q, k, _ = qkv(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=5)
+    v = torch.zeros(B, Hkv, T, D, dtype=torch.bfloat16, device=DEV)
+    v[:, 0] = 1.0
+    v[:, 1] = 2.0
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    for hq in range(Hq):
+        assert torch.all(out[0, hq] == (1.0 if hq < 4 else 2.0)), hq
+
+
+def test_cfg4_full_size(gpu_pkg):
+    """BASELINE config 4 (B4, T2048, 32/8 heads, D128, bf16, causal); oracle on a head subset."""
+    announce("prefill config 4 full size")
+    from importlib import import_module
+    syn = import_module("simple-inference-autoresearch_amd.synthetic")
+    q, k, v = syn.cfg4(DEV)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    worst = 0.0
+    for b, hq in ((0, 0), (1, 7), (2, 18), (3, 31)):
+        hkv = hq // 4
+        ref = O.flash_attention(f64(q[b:b + 1, hq:hq + 1]), f64(k[b:b + 1, hkv:hkv + 1]),
+                                f64(v[b:b + 1, hkv:hkv + 1]), True)
+        worst = max(worst, check(out[b:b + 1, hq:hq + 1], ref, f"cfg4 b={b} hq={hq}"))
+    print(f"cfg4 max abs err on 4 heads: {worst:.3e}")
+
+
+def test_prefill_errors(gpu_pkg):
+    announce("prefill errors")
+    q, k, v = qkv(1, 4, 2, 8, 8, 128, torch.bfloat16, seed=1)
+    with pytest.raises(AssertionError):
+        gpu_pkg.attention_flash_triton(q[..., :48], k[..., :48], v[..., :48], causal=True)
+    with pytest.raises(ValueError):
+        gpu_pkg.attention_flash_triton(q, k, v.to(torch.float16), causal=True)
