@@ -76,22 +76,28 @@ template <int D>
 __device__ __forceinline__ void load_kv_block(const PrefillArgs& a, const char* kb, const char* vb, int key0,
                                               KvRegs<D>& r) {
   const int t = threadIdx.x;
+  const bool full = key0 + kPfBN <= a.Tk;          // uniform: no per-key predicate needed
   {
     const int key = key0 + (t >> 2);
     const int d0 = (t & 3) * (D / 4);
+    const char* src = kb + (int64_t)(full ? key : min(key, a.Tk - 1)) * a.k_sn + d0 * 2;
 #pragma unroll
-    for (int c = 0; c < KvRegs<D>::KCH; ++c)
-      r.k[c] = key < a.Tk ? *(const u32x4*)(kb + (int64_t)key * a.k_sn + (d0 + 8 * c) * 2) : u32x4{0u, 0u, 0u, 0u};
+    for (int c = 0; c < KvRegs<D>::KCH; ++c) {
+      const u32x4 x = *(const u32x4*)(src + 16 * c);
+      r.k[c] = (full || key < a.Tk) ? x : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 #pragma unroll
   for (int g = 0; g < KvRegs<D>::VGRP; ++g) {
     const int idx = t + 256 * g;
     const int c8 = idx % (D / 8), kg = idx / (D / 8);
+    if (kg < 16) {
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int key = key0 + 4 * kg + rr;
-      r.v[g][rr] = (kg < 16 && key < a.Tk) ? *(const u32x4*)(vb + (int64_t)key * a.v_sn + c8 * 16)
-                                           : u32x4{0u, 0u, 0u, 0u};
+      for (int rr = 0; rr < 4; ++rr) {
+        const int key = key0 + 4 * kg + rr;
+        const u32x4 x = *(const u32x4*)(vb + (int64_t)(full ? key : min(key, a.Tk - 1)) * a.v_sn + c8 * 16);
+        r.v[g][rr] = (full || key < a.Tk) ? x : u32x4{0u, 0u, 0u, 0u};
+      }
     }
   }
 }
@@ -185,85 +191,96 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int e = 0; e < ET; ++e) o[e] = f32x16{};
   float m = -INFINITY, l = 0.f;
 
-  KvRegs<D> kv;
+  // Two register staging sets: block it+2 is requested while block it is
+  // computed and block it+1 (already in registers) is written to LDS after it.
+  KvRegs<D> kvA, kvB;
   if (nblk > 0) {
-    load_kv_block<D>(a, kb, vb, 0, kv);
-    store_kv_block<D, T>(kv, lk[0], lv[0]);
+    load_kv_block<D>(a, kb, vb, 0, kvA);
+    store_kv_block<D, T>(kvA, lk[0], lv[0]);
   }
+  if (nblk > 1) load_kv_block<D>(a, kb, vb, kPfBN, kvB);
   __syncthreads();
 
-  for (int it = 0; it < nblk; ++it) {
+  auto step = [&](int it, KvRegs<D>& refill, const KvRegs<D>& next) {
     const int buf = it & 1;
     const int key0 = it * kPfBN;
-    if (it + 1 < nblk) load_kv_block<D>(a, kb, vb, key0 + kPfBN, kv);   // in flight during compute
-    if (key0 < wend) {
-      const uint16_t* K = lk[buf];
-      const uint16_t* V = lv[buf];
-      // ---- S^T = K Q^T for keys [key0, key0 + 64): two 32-key tiles
-      f32x16 s0 = f32x16{}, s1 = f32x16{};
-#pragma unroll
-      for (int j = 0; j < KST; ++j) {
-        const u32x4 a0 = *(const u32x4*)(K + l32 * L::KROW + 16 * j + 8 * h);
-        const u32x4 a1 = *(const u32x4*)(K + (32 + l32) * L::KROW + 16 * j + 8 * h);
-        s0 = mfma32x32x16(T{}, a0, qop[j], s0);
-        s1 = mfma32x32x16(T{}, a1, qop[j], s1);
-      }
-      float sc[32];
-#pragma unroll
-      for (int j = 0; j < 16; ++j) { sc[j] = s0[j] * a.qk_scale; sc[16 + j] = s1[j] * a.qk_scale; }
-      // mask keys past Tk and, on the causal diagonal, keys after the row's position
-      const bool need_mask = key0 + kPfBN > a.Tk || (a.causal && key0 + kPfBN - 1 > off + wrow0);
-      if (need_mask) {
-        const int lim = a.causal ? min(a.Tk - 1, off + qi) : a.Tk - 1;
-#pragma unroll
-        for (int j = 0; j < 32; ++j) {
-          const int key = key0 + (j >> 4) * 32 + ((j & 15) >> 2) * 8 + 4 * h + (j & 3);
-          if (key > lim) sc[j] = -INFINITY;
+    if (it + 2 < nblk) load_kv_block<D>(a, kb, vb, key0 + 2 * kPfBN, refill);
+      if (key0 < wend) {
+        const uint16_t* K = lk[buf];
+        const uint16_t* V = lv[buf];
+        // ---- S^T = K Q^T for keys [key0, key0 + 64): two 32-key tiles
+        f32x16 s0 = f32x16{}, s1 = f32x16{};
+  #pragma unroll
+        for (int j = 0; j < KST; ++j) {
+          const u32x4 a0 = *(const u32x4*)(K + l32 * L::KROW + 16 * j + 8 * h);
+          const u32x4 a1 = *(const u32x4*)(K + (32 + l32) * L::KROW + 16 * j + 8 * h);
+          s0 = mfma32x32x16(T{}, a0, qop[j], s0);
+          s1 = mfma32x32x16(T{}, a1, qop[j], s1);
         }
-      }
-      float lmax = sc[0];
-#pragma unroll
-      for (int j = 1; j < 32; ++j) lmax = fmaxf(lmax, sc[j]);
-      lmax = fmaxf(lmax, __shfl_xor(lmax, 32));          // the partner lane holds the other 32 keys
-      if (__any(lmax > m + 8.0f)) {                      // lazy max (p <= 2^8 otherwise)
-        const float m_new = fmaxf(m, lmax);
-        const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m - m_new);   // row still sees nothing
-        m = m_new;
-        l *= alpha;
-#pragma unroll
-        for (int e = 0; e < ET; ++e) o[e] *= alpha;
-      }
-      const float mu = m == -INFINITY ? 0.f : m;         // rows with nothing visible yet
-      u32x4 pop[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int j0 = (ks >> 1) * 16 + (ks & 1) * 8 + 2 * i;
-          const float p0 = fast_exp2(sc[j0] - mu), p1 = fast_exp2(sc[j0 + 1] - mu);
-          const uint32_t w = pack2(F16{}, p0, p1);
-          // normalise by the rounded weights the MFMA actually uses: the output
-          // stays an exact convex combination of V rows
-          l += lo_f32(F16{}, w) + hi_f32(F16{}, w);
-          pop[ks][i] = w;
+        // raw scores; the scale is folded into the exponent (c > 0 keeps the max)
+        float sc[32];
+  #pragma unroll
+        for (int j = 0; j < 16; ++j) { sc[j] = s0[j]; sc[16 + j] = s1[j]; }
+        // mask keys past Tk and, on the causal diagonal, keys after the row's position
+        const bool need_mask = key0 + kPfBN > a.Tk || (a.causal && key0 + kPfBN - 1 > off + wrow0);
+        if (need_mask) {
+          const int lim = a.causal ? min(a.Tk - 1, off + qi) : a.Tk - 1;
+  #pragma unroll
+          for (int j = 0; j < 32; ++j) {
+            const int key = key0 + (j >> 4) * 32 + ((j & 15) >> 2) * 8 + 4 * h + (j & 3);
+            if (key > lim) sc[j] = -INFINITY;
+          }
         }
-      }
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int e = 0; e < ET; ++e) {
-#pragma unroll
+        float rmax = fmaxf(sc[0], sc[1]);
+  #pragma unroll
+        for (int j = 2; j < 32; j += 2) rmax = fmaxf(rmax, fmaxf(sc[j], sc[j + 1]));
+        rmax = fmaxf(rmax, __shfl_xor(rmax, 32));         // the partner lane holds the other 32 keys
+        const float smax = rmax * a.qk_scale;
+        if (__any(smax > m + 8.0f)) {                      // lazy max (p <= 2^8 otherwise)
+          const float m_new = fmaxf(m, smax);
+          const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m - m_new);   // row still sees nothing
+          m = m_new;
+          l *= alpha;
+  #pragma unroll
+          for (int e = 0; e < ET; ++e) o[e] *= alpha;
+        }
+        const float mu = m == -INFINITY ? 0.f : m;         // rows with nothing visible yet
+        const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+        u32x4 pop[4];
+  #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const uint16_t* vp = V + (32 * e + l32) * L::VROW + (ks >> 1) * 32 + (ks & 1) * 16 + 4 * h;
-          const u32x2 lo = *(const u32x2*)vp;
-          const u32x2 hi = *(const u32x2*)(vp + 8);
-          const u32x4 va = u32x4{lo[0], lo[1], hi[0], hi[1]};
-          o[e] = mfma32x32x16(F16{}, va, pop[ks], o[e]);
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int j0 = (ks >> 1) * 16 + (ks & 1) * 8 + 2 * i;
+            const float p0 = fast_exp2(__builtin_fmaf(sc[j0], a.qk_scale, -mu));
+            const float p1 = fast_exp2(__builtin_fmaf(sc[j0 + 1], a.qk_scale, -mu));
+            const uint32_t w = pack2(F16{}, p0, p1);
+            // the row sum is taken over the rounded weights the MFMA uses, so the
+            // output stays an exact convex combination of V rows
+            l = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, l, false);
+            pop[ks][i] = w;
+          }
+        }
+        // ---- O^T += V^T P^T
+  #pragma unroll
+        for (int e = 0; e < ET; ++e) {
+  #pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const uint16_t* vp = V + (32 * e + l32) * L::VROW + (ks >> 1) * 32 + (ks & 1) * 16 + 4 * h;
+            const u32x2 lo = *(const u32x2*)vp;
+            const u32x2 hi = *(const u32x2*)(vp + 8);
+            const u32x4 va = u32x4{lo[0], lo[1], hi[0], hi[1]};
+            o[e] = mfma32x32x16(F16{}, va, pop[ks], o[e]);
+          }
         }
       }
-    }
     // buffer buf^1 was last read before the previous barrier: refill it now
-    if (it + 1 < nblk) store_kv_block<D, T>(kv, lk[buf ^ 1], lv[buf ^ 1]);
+    if (it + 1 < nblk) store_kv_block<D, T>(next, lk[buf ^ 1], lv[buf ^ 1]);
     __syncthreads();
+  };
+  for (int it = 0; it < nblk; it += 2) {
+    step(it, kvA, kvB);
+    if (it + 1 < nblk) step(it + 1, kvB, kvA);
   }
 
   // ---- normalise and store: lane owns query qi, d = 32 e + 8 (j / 4) + 4 h + j % 4
