@@ -12,8 +12,9 @@
  *    the shape and the strides in ELEMENTS (a torch view maps 1:1).  The last
  *    (head_dim) stride must be 1; other strides may describe any view.
  *  - Nothing here allocates device memory, synchronises, or keeps per-call
- *    state: callers own every buffer.  Split-K decode needs a caller-provided
- *    workspace whose size `sia_decode_workspace_size` reports.
+ *    state: callers own every buffer.  Split-K decode and prefill need a
+ *    caller-provided workspace whose size `sia_decode_workspace_size` /
+ *    `sia_prefill_workspace_size` reports.
  *  - Work is enqueued asynchronously on `stream` (a hipStream_t; NULL = the
  *    null stream), so every entry point may be captured in a HIP graph.
  *    `kv_len` is always read on the device.
@@ -136,9 +137,18 @@ int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_poo
  * 16-byte aligned rows; out (B,Hq,Tq,D) view in q's dtype -- a transposed
  * view of a (B,Tq,Hq,D) buffer gives the reference's out_token_major layout.
  * causal != 0 applies the bottom-right mask: row i sees keys <= (Tk-Tq)+i;
- * rows that see no key are written as zeros.  head_dim 64 or 128. */
+ * rows that see no key are written as zeros.  head_dim 64 or 128.
+ * workspace: device memory of at least sia_prefill_workspace_size bytes
+ * (256-byte aligned); it holds V converted to f16 in the kernel's block
+ * layout and is free again when the stream passes the call. */
 int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
-                            float sm_scale, const sia_tensor* out, void* stream);
+                            float sm_scale, const sia_tensor* out, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
+/* Workspace bytes sia_attention_flash_fwd needs for v of shape
+ * (batch, kv_heads, kv_len, head_dim).  No reference counterpart: the
+ * reference's Triton launch allocates nothing (kernels/attention_kernel.py:296). */
+int sia_prefill_workspace_size(int64_t batch, int64_t kv_heads, int64_t kv_len, int64_t head_dim, size_t* bytes);
 
 #ifdef __cplusplus
 }

@@ -23,7 +23,7 @@ from .decode import (
     paged_attention_flash_decode,
     paged_gqa_int8_flash_decode,
 )
-from .prefill import attention_flash_triton
+from .prefill import attention_flash_triton, prefill_workspace_size
 
 __all__ = [
     "LibraryMissing",
@@ -39,5 +39,6 @@ __all__ = [
     "load_library",
     "paged_attention_flash_decode",
     "paged_gqa_int8_flash_decode",
+    "prefill_workspace_size",
     "require_library",
 ]

@@ -1,4 +1,4 @@
-// extern "C" prefill entry point: validation and dispatch.
+// extern "C" prefill entry points: validation, workspace size and dispatch.
 #include <math.h>
 #include <string.h>
 
@@ -19,10 +19,27 @@ int check4(const sia_tensor* t, const char* name) {
   return SIA_OK;
 }
 
+// V^T block images: one f16 (64 x head_dim) image per 64-key block of every (b, kv head).
+int64_t image_bytes(int64_t B, int64_t Hkv, int64_t Tk, int64_t D) {
+  const int64_t nkb = (Tk + kPfBN - 1) / kPfBN;
+  return B * Hkv * nkb * kPfBN * D * 2;
+}
+
 }  // namespace
 
+extern "C" int sia_prefill_workspace_size(int64_t batch, int64_t kv_heads, int64_t kv_len, int64_t head_dim,
+                                          size_t* bytes) {
+  if (bytes == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  if (batch <= 0 || kv_heads <= 0 || kv_len < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (64, 128)", (long long)head_dim);
+  *bytes = (size_t)image_bytes(batch, kv_heads, kv_len, head_dim);
+  return SIA_OK;
+}
+
 extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
-                                       float sm_scale, const sia_tensor* out, void* stream) {
+                                       float sm_scale, const sia_tensor* out, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
   int rc;
   if ((rc = check4(q, "q")) || (rc = check4(k, "k")) || (rc = check4(v, "v")) || (rc = check4(out, "out"))) return rc;
   if (q->dtype != SIA_F16 && q->dtype != SIA_BF16)
@@ -40,7 +57,16 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   if (Hq % Hkv) return fail(SIA_ERR_INVALID_ARGUMENT, "Hq must be a multiple of Hkv");
   if (D != 64 && D != 128) return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (64, 128)", (long long)D);
   if (Tq > (1 << 30) || Tk > (1 << 30)) return fail(SIA_ERR_UNSUPPORTED, "sequence too long");
+  // K rows are fetched by 32-bit buffer offsets of up to 64 rows from a block start
+  const int64_t k_sn = bstride(k, 2);
+  if (Tk > 1 && (k_sn < 2 * D || k_sn * kPfBN >= ((int64_t)1 << 31)))
+    return fail(SIA_ERR_UNSUPPORTED, "k token stride %lld bytes: expected [%lld, 2^31/64)", (long long)k_sn,
+                (long long)(2 * D));
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return fail(SIA_ERR_INVALID_ARGUMENT, "sm_scale must be positive");
+  const int64_t need = image_bytes(B, Hkv, Tk, D);
+  if (need > 0 && (workspace == nullptr || (uintptr_t)workspace % 256 || workspace_bytes < (size_t)need))
+    return fail(SIA_ERR_WORKSPACE, "prefill workspace missing, misaligned or smaller than %lld bytes",
+                (long long)need);
   const DeviceInfo& dev = device_info();
   if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
   if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
@@ -50,16 +76,24 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   memset(&L, 0, sizeof(L));
   PrefillArgs& a = L.a;
   a.q = (const char*)q->data; a.q_sb = bstride(q, 0); a.q_sh = bstride(q, 1); a.q_sm = bstride(q, 2);
-  a.k = (const char*)k->data; a.k_sb = bstride(k, 0); a.k_sh = bstride(k, 1); a.k_sn = bstride(k, 2);
-  a.v = (const char*)v->data; a.v_sb = bstride(v, 0); a.v_sh = bstride(v, 1); a.v_sn = bstride(v, 2);
+  a.k = (const char*)k->data; a.k_sb = bstride(k, 0); a.k_sh = bstride(k, 1); a.k_sn = k_sn;
+  a.vimg = (const char*)workspace;
   a.out = (char*)out->data; a.o_sb = bstride(out, 0); a.o_sh = bstride(out, 1); a.o_sm = bstride(out, 2);
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.Tq = (int)Tq; a.Tk = (int)Tk;
   a.causal = causal != 0;
   a.qk_scale = sm_scale * 1.4426950408889634f;
   a.nqblk = (int)((Tq + kPfBM - 1) / kPfBM);
+  a.nkb = (int)((Tk + kPfBN - 1) / kPfBN);
   const int64_t groups = (int64_t)a.nqblk * B * Hkv;   // work-groups come in runs of G sharing a KV head
   if (groups * a.G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "grid too large");
   a.remap = groups % 8 == 0;
+
+  PackArgs& p = L.pack;
+  p.v = (const char*)v->data; p.v_sb = bstride(v, 0); p.v_sh = bstride(v, 1); p.v_sn = bstride(v, 2);
+  p.vimg = (char*)workspace;
+  p.Hkv = (int)Hkv; p.Tk = (int)Tk; p.nkb = a.nkb;
+  p.nblocks = B * Hkv * a.nkb;
+  if (p.nblocks * D / 256 + 1 > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "K/V too large");
   L.D = (int)D;
   L.dtype = q->dtype;
   L.stream = (hipStream_t)stream;

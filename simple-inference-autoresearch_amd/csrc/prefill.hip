@@ -7,6 +7,11 @@ namespace sia {
 
 template <int D, class T>
 static int launch_prefill_typed(PrefillLaunch& L) {
+  if (L.pack.nblocks > 0) {
+    const int64_t threads = L.pack.nblocks * D;   // one thread per (image chunk, 8 dims)
+    hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, L.stream,
+                       L.pack);
+  }
   const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
   hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(256), 0, L.stream, L.a);
   const hipError_t e = hipGetLastError();

@@ -7,6 +7,7 @@ namespace sia {
 
 struct PrefillLaunch {
   PrefillArgs a;
+  PackArgs pack;   // V -> f16 V^T block images (run first on the same stream)
   int D;
   int dtype;
   hipStream_t stream;

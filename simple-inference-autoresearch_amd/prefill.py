@@ -11,6 +11,7 @@ which is kept so callers need no change.
 from __future__ import annotations
 
 import ctypes
+import functools
 
 import torch
 
@@ -19,11 +20,23 @@ from . import _lib
 _HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
+@functools.lru_cache(maxsize=256)
+def prefill_workspace_size(batch: int, kv_heads: int, kv_len: int, head_dim: int) -> int:
+    """Bytes of device workspace ``sia_attention_flash_fwd`` needs (f16 V^T block images)."""
+    h = _lib.require_library()
+    n = ctypes.c_size_t(0)
+    _lib.check(h.sia_prefill_workspace_size(batch, kv_heads, kv_len, head_dim, ctypes.byref(n)))
+    return int(n.value)
+
+
 def _supported_view(t: torch.Tensor) -> bool:
     if t.stride(-1) != 1 or t.data_ptr() % 16:
         return False
     es = t.element_size()
-    return all((s * es) % 16 == 0 for s in t.stride()[:-1])
+    if not all((s * es) % 16 == 0 for s in t.stride()[:-1]):
+        return False
+    # K/V rows are fetched with 32-bit offsets of up to 64 rows from a block start
+    return t.shape[-2] <= 1 or t.shape[-1] * es <= t.stride(-2) * es < (1 << 31) // 64
 
 
 def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool,
@@ -56,9 +69,12 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
         else:
             out = torch.empty((B, Hq, Tq, D), dtype=q.dtype, device=q.device)
             out_view = out
+        nbytes = prefill_workspace_size(B, Hkv, Tk, D)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         dq, dk, dv, do = (_lib.desc(t) for t in (q, k, v, out_view))
         rc = h.sia_attention_flash_fwd(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv),
                                        ctypes.c_int32(1 if causal else 0), ctypes.c_float(float(sm_scale)),
-                                       ctypes.byref(do), ctypes.c_void_p(_lib.stream_handle(q.device)))
+                                       ctypes.byref(do), ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(nbytes),
+                                       ctypes.c_void_p(_lib.stream_handle(q.device)))
         _lib.check(rc)
     return out
