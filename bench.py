@@ -186,6 +186,32 @@ def bench_prefill_config(pkg, steps: int, warmup: int):
             "algorithmic_flops": flops, "workload": "config 4: causal prefill bf16 B4 T2048 32/8 heads D128"}
 
 
+def bench_copy(steps: int, warmup: int, nbytes: int = 1 << 30):
+    """A plain device-to-device copy of `nbytes` (torch's copy kernel).
+
+    Reads and writes exactly `nbytes` per launch, so rocprofv3's FETCH_SIZE /
+    WRITE_SIZE for it give the counters' scale against known HBM traffic; its
+    rate is also the practically reachable streaming bandwidth.
+    """
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "us_per_call": round(ms * 1e3, 2),
+            "GBps_read_plus_write": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def load_traffic(kernel: str):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE/WRITE_SIZE (profiles/), or None."""
     path = os.path.join(ROOT, "profiles", f"{kernel}_traffic.json")
@@ -203,8 +229,9 @@ def main(argv=None):
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--no-others", action="store_true", help="skip configs 2, 4 and 5")
-    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5"],
-                   help="decode config to run as the headline (profiling runs)")
+    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "copy"],
+                   help="config to run alone (profiling runs); 'copy' is a plain 1 GiB device copy "
+                        "that calibrates the HBM byte counters")
     args = p.parse_args(argv)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -221,6 +248,10 @@ def main(argv=None):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.config == "copy":   # counter calibration: 1 GiB read + 1 GiB written per launch
+        r = bench_copy(args.steps, args.warmup)
+        print(json.dumps({"config": "copy", **r}), flush=True)
+        return 0
     if args.config == "cfg4":   # prefill only (profiling runs)
         r = bench_prefill_config(pkg, args.steps, args.warmup)
         print(f"[bench] cfg4: {r}", file=sys.stderr, flush=True)
