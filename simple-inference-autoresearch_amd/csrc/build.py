@@ -84,7 +84,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed for: {', '.join(failed)}")
     lib = os.path.join(PKG, LIB_NAME)
     tmp = lib + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    # -z defs: every symbol must resolve at link time (a kernel whose host-side
+    # launch stub was not emitted fails here instead of at load time)
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)

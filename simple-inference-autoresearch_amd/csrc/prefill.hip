@@ -13,7 +13,7 @@ static int launch_prefill_typed(PrefillLaunch& L) {
                        L.pack);
   }
   const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
-  hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(256), 0, L.stream, L.a);
+  hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(kPfWaves * 64), 0, L.stream, L.a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
   return SIA_OK;

@@ -15,19 +15,24 @@
 //    one 64-key block per image, laid out exactly as the main kernel's LDS
 //    wants it, so no work-group converts or transposes V again (each V block
 //    is read by every query block and every query head of its KV head).
-//  * A work-group of prefill_fwd is 4 waves x 32 query rows (BM = 128) of one
-//    (b, hq); it walks key blocks of BN = 64 through two LDS stages filled by
-//    buffer_load ... lds (global -> LDS DMA: no VGPR staging, no VALU), the
-//    next block's DMA in flight while the current one is computed.
-//  * LDS is chunk-major: the 16-byte chunk c of row r sits at byte
-//    c * rows * 16 + r * 16, so the 32 lanes that read one MFMA operand read
-//    32 consecutive chunks (no bank conflict, no swizzle arithmetic) and
-//    every LDS address is a per-lane base plus an immediate.
+//  * A work-group of prefill_fwd is 8 waves x 32 query rows (BM = 256) of one
+//    (b, hq), two waves per SIMD.  It walks key blocks of BN = 64 through a
+//    four-stage LDS ring per tensor filled by buffer_load ... lds (global ->
+//    LDS DMA, no VGPR staging): three blocks are in flight while one is
+//    computed, every wait is a constant vmcnt, and the per-step barrier
+//    carries no memory fence (a fence would drain the ring).
+//  * K stages are row-major with an XOR swizzle of their 16-byte chunks, so
+//    each DMA instruction reads whole rows (coalesced) and the MFMA operand
+//    reads stay free of bank conflicts; V^T images are chunk-major.
 //  * Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16 (keys as rows,
 //    its 32 queries as columns), so every lane owns one query: the row max is
 //    a lane-local v_maximum3 tree plus one v_permlane32_swap, and P^T feeds
 //    O^T += V^T P^T straight from registers (the key order of its k-slots
 //    matches the S^T output layout; the V^T images store keys in that order).
+//  * Software pipeline: the MFMAs of the next block's scores are interleaved
+//    (sched_group_barrier) with the exponentials of the current block, whose
+//    PV MFMAs follow; the loop is unrolled by four so stage arrays and score
+//    registers are fixed per step at compile time.
 //  * Blocks are issued heaviest-first (the causal diagonal makes late query
 //    blocks the longest), and the query heads that share a KV head are placed
 //    on the same XCD so their K/V tiles are served by one L2.
@@ -67,8 +72,10 @@ struct PackArgs {
   int64_t nblocks;                              // B * Hkv * nkb
 };
 
-constexpr int kPfBM = 128;   // query rows per work-group (4 waves x 32)
-constexpr int kPfBN = 64;    // keys per block
+constexpr int kPfWaves = 8;             // waves per work-group (two per SIMD)
+constexpr int kPfBM = 32 * kPfWaves;    // query rows per work-group (32 per wave)
+constexpr int kPfBN = 64;               // keys per block
+constexpr int kPfStages = 4;            // K and V LDS ring depth: three blocks in flight
 constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (32-bit data, no swizzle)
 
 // Bytes of one K block (64 rows of D) and of one V^T block image.
@@ -123,9 +130,9 @@ __global__ __launch_bounds__(256) void prefill_pack_v(const PackArgs a) {
   }
 }
 
-template <int S>
-struct PfStage {
-  static constexpr int value = S;
+template <int P>
+struct PfParity {
+  static constexpr int value = P;
 };
 
 // Combine lanes l and l ^ 32 (the two halves of the wave) without LDS:
@@ -142,15 +149,51 @@ __device__ __forceinline__ float half_swap_sum(float x) {
   return __builtin_bit_cast(float, (uint32_t)r[0]) + __builtin_bit_cast(float, (uint32_t)r[1]);
 }
 
+// Work-group barrier for the K/V ring.  __syncthreads() carries a release
+// fence, which on this target waits for every DMA still in flight (vmcnt(0))
+// and would drain the ring each step.  The hand-offs here are ordered
+// explicitly instead: a stage's DMA is retired by the wave's own vmcnt wait
+// before it arrives, and its LDS reads of a stage are complete (lgkmcnt(0))
+// before another wave may refill it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// vmcnt(n) for a wave-uniform n in [0, 8] (the immediate must be a constant)
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0f70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0f71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0f72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0f73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0f74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0f75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0f76); break;
+    case 7: __builtin_amdgcn_s_waitcnt(0x0f77); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0f78); break;
+  }
+}
+
 template <int D, class T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void prefill_fwd(const PrefillArgs a) {
+__global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void prefill_fwd(const PrefillArgs a) {
   constexpr int KST = D / 16;                   // QK k-steps
   constexpr int ET = D / 32;                    // O^T d-tiles
   constexpr int BLK = pf_block_bytes<D>();
-  constexpr int NDMA = BLK / 1024 / 4;          // 1 KB DMA instructions per wave per tensor and block
-  // chunk-major stages: K chunk c of key row r at c * 1024 + r * 16 (64 rows);
-  // V^T image chunk c of dimension d at c * D * 16 + d * 16
-  __shared__ __attribute__((aligned(1024))) char lk0[BLK], lk1[BLK], lv0[BLK], lv1[BLK];
+  constexpr int NDMA = BLK / 1024 / kPfWaves;   // 1 KB DMA instructions per wave per tensor and block
+  static_assert(NDMA >= 1 && 2 * NDMA * 2 <= 8, "DMA split");
+  // K stages: swizzled row-major (below); V^T image chunk c of dimension d at
+  // c * D * 16 + d * 16
+  // (distinct arrays per stage: the compiler then sees that a DMA into one
+  // stage never aliases the LDS reads of another and adds no waits)
+  __shared__ __attribute__((aligned(1024))) char lk0[BLK], lk1[BLK], lk2[BLK], lk3[BLK];
+  __shared__ __attribute__((aligned(1024))) char lv0[BLK], lv1[BLK], lv2[BLK], lv3[BLK];
+  static_assert(kPfStages == 4, "four stage arrays");
+  auto kstage = [&](auto s) -> char* {
+    constexpr int S = decltype(s)::value & 3;
+    return S == 0 ? lk0 : S == 1 ? lk1 : S == 2 ? lk2 : lk3;
+  };
+  auto vstage = [&](auto s) -> char* {
+    constexpr int S = decltype(s)::value & 3;
+    return S == 0 ? lv0 : S == 1 ? lv1 : S == 2 ? lv2 : lv3;
+  };
 
   // ---- block -> (query block, b, hq), heaviest first, KV-head groups per XCD
   int lin = blockIdx.x;
@@ -182,28 +225,65 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   }
 
   const int kend = a.causal ? min(a.Tk, off + q0 + kPfBM) : a.Tk;
-  const int nblk = kend > 0 ? (kend + kPfBN - 1) / kPfBN : 0;
+  const int nblk = kend > 0 ? (kend + kPfBN - 1) / kPfBN : 0;   // key blocks of the work-group
   const int wrow0 = q0 + wave * 32;                      // this wave's first row
   const int wend = a.causal ? min(a.Tk, off + wrow0 + 32) : a.Tk;   // keys this wave can see
+  const int wblk = wend > 0 ? min(nblk, (wend + kPfBN - 1) / kPfBN) : 0;   // blocks this wave computes
+  // blocks [0, wfull) are visible to every row of the wave: no mask
+  const int lim_all = a.causal ? min(a.Tk - 1, off + wrow0) : a.Tk - 1;
+  const int wfull = lim_all >= 0 ? (lim_all + 1) / kPfBN : 0;
+  const int lim = a.causal ? min(a.Tk - 1, off + qi) : a.Tk - 1;   // this lane's last visible key
 
   const char* kb = a.k + b * a.k_sb + (int64_t)hkv * a.k_sh;
   const char* vimg = a.vimg + ((int64_t)b * a.Hkv + hkv) * a.nkb * BLK;
-  const int k_voff = lane * (int)a.k_sn;                // DMA lane = key row
+  // K stages are row-major with an XOR swizzle: 16-byte chunk c of key row r
+  // sits in slot c ^ (r % NC) of the row's RB bytes.  A DMA instruction then
+  // reads whole rows (16 lanes per 256-byte row at D = 128: coalesced), and
+  // the 8 lanes an LDS read serves at a time, which hold 8 consecutive rows,
+  // hit 8 different bank groups.  k_voff[i]: this lane's byte offset inside
+  // the block for DMA instruction i of the wave.
+  constexpr int RB = 2 * D, NC = D / 8, ROWS_PER_DMA = 1024 / RB;
+  int k_voff[NDMA];
+#pragma unroll
+  for (int i = 0; i < NDMA; ++i) {
+    const int r = (wave * NDMA + i) * ROWS_PER_DMA + lane / NC;
+    k_voff[i] = r * (int)a.k_sn + (((lane % NC) ^ (r % NC)) * 16);
+  }
+  // QK operand addresses: k-step j reads chunk 2 j + h of row l32 (tile 0)
+  // and row l32 + 32 (tile 1: + 32 RB, same swizzle since 32 % NC == 0)
+  int k_rd[KST];
+#pragma unroll
+  for (int j = 0; j < KST; ++j) k_rd[j] = l32 * RB + (((2 * j + h) ^ (l32 % NC)) * 16);
 
-  // DMA of block `blk` into one stage: wave w moves K chunks [w NDMA, (w+1) NDMA)
-  // (64 rows each; rows past Tk read as zero through the buffer bound) and the
-  // same range of 1 KB pieces of the V^T image.
-  auto issue = [&](int blk, char* LK, char* LV) {
-    const int key0 = blk * kPfBN;
-    const int rows = min(kPfBN, a.Tk - key0);
+  // DMA of K block `blk` / V^T image `blk` into its ring stage (blk % 4):
+  // wave w moves chunks [w NDMA, (w+1) NDMA) (64 rows each; rows past Tk read
+  // as zero through the buffer bound) and the same range of 1 KB pieces of
+  // the image.  A block past the work-group's last one is issued with an
+  // empty buffer range: the hardware drops every out-of-range read (no memory
+  // traffic) and the stage it fills is never used, so every DMA group has the
+  // same instruction count and the waits below are constants.
+  auto issue_k = [&](int blk, char* LK) {
+    const bool live = blk < nblk;
+    const int key0 = live ? blk * kPfBN : 0;
+    const int rows = live ? min(kPfBN, a.Tk - key0) : 0;
     const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(kb + (int64_t)key0 * a.k_sn), 0, rows * (int)a.k_sn, kBufferFlags);
-    const __amdgpu_buffer_rsrc_t rv =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(vimg + (int64_t)blk * BLK), 0, BLK, kBufferFlags);
 #pragma unroll
     for (int i = 0; i < NDMA; ++i) {
       const int c = wave * NDMA + i;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, LK + c * 1024, 16, k_voff, c * 16, 0, 0);
+      // (through a local: an array element passed straight to this builtin makes
+      // the host pass drop the kernel's launch stub)
+      const int voff = k_voff[i];
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, LK + c * 1024, 16, voff, 0, 0, 0);
+    }
+  };
+  auto issue_v = [&](int blk, char* LV) {
+    const bool live = blk < nblk;
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(vimg + (live ? (int64_t)blk * BLK : 0)), 0, live ? BLK : 0, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < NDMA; ++i) {
+      const int c = wave * NDMA + i;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, LV + c * 1024, 16, lane * 16, c * 1024, 0, 0);
     }
   };
@@ -213,44 +293,50 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
   for (int e = 0; e < ET; ++e) o[e] = f32x16{};
   float m = -INFINITY, l = 0.f;
 
-  auto compute = [&](const char* K, const char* V, int key0) {
-    // ---- S^T = K Q^T for keys [key0, key0 + 64): two 32-key tiles
-    f32x16 s0 = f32x16{}, s1 = f32x16{};
-    const char* kr = K + h * 1024 + l32 * 16;
+  // S^T = K Q^T for the 64 keys of one K stage: two 32-key tiles (raw scores;
+  // the scale is folded into the exponent, c > 0 keeps the max)
+  auto qk = [&](const char* K, f32x16& s0, f32x16& s1) {
+    s0 = f32x16{};
+    s1 = f32x16{};
 #pragma unroll
     for (int j = 0; j < KST; ++j) {
-      const u32x4 a0 = *(const u32x4*)(kr + j * 2048);
-      const u32x4 a1 = *(const u32x4*)(kr + j * 2048 + 512);
+      const u32x4 a0 = *(const u32x4*)(K + k_rd[j]);
+      const u32x4 a1 = *(const u32x4*)(K + k_rd[j] + 32 * RB);
       s0 = mfma32x32x16(T{}, a0, qop[j], s0);
       s1 = mfma32x32x16(T{}, a1, qop[j], s1);
     }
-    // raw scores; the scale is folded into the exponent (c > 0 keeps the max)
-    float sc[32];
+  };
+  // keys past this lane's last visible key -> -inf (diagonal / ragged blocks)
+  auto mask = [&](f32x16& s0, f32x16& s1, int key0) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) { sc[j] = s0[j]; sc[16 + j] = s1[j]; }
-    // mask keys past Tk and, on the causal diagonal, keys after the row's position
-    const bool need_mask = key0 + kPfBN > a.Tk || (a.causal && key0 + kPfBN - 1 > off + wrow0);
-    if (need_mask) {
-      const int lim = a.causal ? min(a.Tk - 1, off + qi) : a.Tk - 1;
-#pragma unroll
-      for (int j = 0; j < 32; ++j) {
-        const int key = key0 + (j >> 4) * 32 + ((j & 15) >> 2) * 8 + 4 * h + (j & 3);
-        if (key > lim) sc[j] = -INFINITY;
-      }
+    for (int j = 0; j < 16; ++j) {
+      const int key = key0 + ((j & 15) >> 2) * 8 + 4 * h + (j & 3);
+      if (key > lim) s0[j] = -INFINITY;
+      if (key + 32 > lim) s1[j] = -INFINITY;
     }
+  };
+  // row max over the 64 keys: a lane-local tree plus the partner half of the wave
+  auto rowmax = [&](const f32x16& s0, const f32x16& s1) {
     float mx[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      mx[j] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(sc[4 * j], sc[4 * j + 1]),
-                                            __builtin_elementwise_maximum(sc[4 * j + 2], sc[4 * j + 3]));
-    float rmax = __builtin_elementwise_maximum(
+    for (int j = 0; j < 4; ++j) {
+      mx[j] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s0[4 * j], s0[4 * j + 1]),
+                                            __builtin_elementwise_maximum(s0[4 * j + 2], s0[4 * j + 3]));
+      mx[4 + j] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s1[4 * j], s1[4 * j + 1]),
+                                                __builtin_elementwise_maximum(s1[4 * j + 2], s1[4 * j + 3]));
+    }
+    const float r = __builtin_elementwise_maximum(
         __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx[0], mx[1]),
                                       __builtin_elementwise_maximum(mx[2], mx[3])),
         __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx[4], mx[5]),
                                       __builtin_elementwise_maximum(mx[6], mx[7])));
-    rmax = half_swap_max(rmax);                        // the partner lane holds the other 32 keys
+    return half_swap_max(r);
+  };
+  // lazy running max: (l, o) are rescaled only when the block max exceeds m by
+  // 2^8 (p <= 2^8 otherwise, well inside f16)
+  auto raise_max = [&](float rmax) {
     const float smax = rmax * a.qk_scale;
-    if (__any(smax > m + 8.0f)) {                      // lazy max (p <= 2^8 otherwise)
+    if (__any(smax > m + 8.0f)) {
       const float m_new = __builtin_elementwise_maximum(m, smax);
       const float alpha = m_new == -INFINITY ? 1.0f : fast_exp2(m - m_new);   // row still sees nothing
       m = m_new;
@@ -258,24 +344,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
 #pragma unroll
       for (int e = 0; e < ET; ++e) o[e] *= alpha;
     }
-    const float mu = m == -INFINITY ? 0.f : m;         // rows with nothing visible yet
+  };
+  // P = 2^(s c - m) rounded to f16, packed as the B operand of the PV product
+  // (k-slot ks holds the keys of S^T output registers 8 (ks % 2) .. + 8 of
+  // tile ks / 2); the row sum is taken over the rounded weights the MFMA
+  // uses, so the output stays an exact convex combination of V rows
+  auto numer = [&](const f32x16& s0, const f32x16& s1, u32x4* pop) {
+    const float mu = m == -INFINITY ? 0.f : m;           // rows with nothing visible yet
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-    u32x4 pop[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int j0 = (ks >> 1) * 16 + (ks & 1) * 8 + 2 * i;
-        const float p0 = fast_exp2(__builtin_fmaf(sc[j0], a.qk_scale, -mu));
-        const float p1 = fast_exp2(__builtin_fmaf(sc[j0 + 1], a.qk_scale, -mu));
+        const int j0 = (ks & 1) * 8 + 2 * i;
+        const float x0 = ks < 2 ? s0[j0] : s1[j0];
+        const float x1 = ks < 2 ? s0[j0 + 1] : s1[j0 + 1];
+        const float p0 = fast_exp2(__builtin_fmaf(x0, a.qk_scale, -mu));
+        const float p1 = fast_exp2(__builtin_fmaf(x1, a.qk_scale, -mu));
         const uint32_t w = pack2(F16{}, p0, p1);
-        // the row sum is taken over the rounded weights the MFMA uses, so the
-        // output stays an exact convex combination of V rows
         l = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, l, false);
         pop[ks][i] = w;
       }
     }
-    // ---- O^T += V^T P^T: operand chunk 2 ks + h of dimension 32 e + l32
+  };
+  // O^T += V^T P^T: operand chunk 2 ks + h of dimension 32 e + l32
+  auto pv = [&](const char* V, const u32x4* pop) {
     const char* vr = V + h * D * 16 + l32 * 16;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -287,28 +380,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void p
     }
   };
 
-  // One pipeline step: start the DMA of block it + 1 into the other stage
-  // (last read before the previous barrier), compute block it, then wait for
-  // this wave's DMA and meet the other waves (their DMA done, their reads of
-  // this stage finished).
-  auto step = [&](auto stage, int it) {
-    constexpr int S = decltype(stage)::value;
-    if (it + 1 < nblk) issue(it + 1, S ? lk0 : lk1, S ? lv0 : lv1);
-    const int key0 = it * kPfBN;
-    if (key0 < wend) compute(S ? lk1 : lk0, S ? lv1 : lv0, key0);
-    __builtin_amdgcn_s_waitcnt(0x0f70);                // vmcnt(0)
-    __syncthreads();
+  // Software pipeline over key blocks.  DMA group g_0 = {K_0, V_0, K_1},
+  // g_x = {K_{x+1}, V_x} (x >= 1); step j consumes g_j (K_{j+1} for the
+  // scores of the next block, V_j for this block's PV) and, after the
+  // barrier that retires step j - 1, refills the stages of K_j and V_{j-1}
+  // with g_{j+3}, so three groups stay in flight.  Within a step the MFMAs
+  // of S_{j+1} run under the softmax of block j.
+  auto step = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1, float& rmax) {
+    wait_vmcnt(4 * NDMA);                                // this wave's part of g_j landed (g_{j+1}, g_{j+2} may fly)
+    ring_barrier();                                      // everyone's part landed; step j - 1 retired
+    constexpr int P = decltype(parity)::value;           // j % 4, known at compile time
+    issue_k(j + 4, kstage(PfParity<P>{}));
+    issue_v(j + 3, vstage(PfParity<P + 3>{}));
+    if (j < wblk) {
+      raise_max(rmax);
+      // S_{j+1} is computed even on the wave's last block (its stage then
+      // holds another block or stale keys and the scores are discarded):
+      // one code path keeps the accumulators in place across iterations
+      u32x4 pop[4];
+      qk(kstage(PfParity<P + 1>{}), sb0, sb1);
+      numer(sa0, sa1, pop);
+      pv(vstage(PfParity<P>{}), pop);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // 4 K operand reads ahead
+#pragma unroll
+      for (int i = 0; i < 2 * KST; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one S MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // next operand read
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // softmax VALU
+      }
+#pragma unroll
+      for (int i = 0; i < 4 * ET; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one PV MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      if (j + 1 >= wfull) mask(sb0, sb1, (j + 1) * kPfBN);
+      rmax = rowmax(sb0, sb1);
+    }
   };
 
+  f32x16 s0 = f32x16{}, s1 = f32x16{}, n0 = f32x16{}, n1 = f32x16{};
+  float rmax = -INFINITY;
   if (nblk > 0) {
-    issue(0, lk0, lv0);
-    __builtin_amdgcn_s_waitcnt(0x0f70);
-    __syncthreads();
+    issue_k(0, lk0);
+    issue_v(0, lv0);
+    issue_k(1, lk1);
+    issue_k(2, lk2);
+    issue_v(1, lv1);
+    issue_k(3, lk3);
+    issue_v(2, lv2);
+    wait_vmcnt(4 * NDMA);                                // g_0 landed
+    ring_barrier();
+    if (wblk > 0) {
+      qk(lk0, s0, s1);
+      if (wfull == 0) mask(s0, s1, 0);
+      rmax = rowmax(s0, s1);
+    }
   }
-  for (int it = 0; it < nblk; it += 2) {
-    step(PfStage<0>{}, it);
-    if (it + 1 < nblk) step(PfStage<1>{}, it + 1);
+  // unrolled by four: stage arrays and the roles of the two score tiles are
+  // fixed per step at compile time
+  int j = 0;
+  for (; j + 3 < nblk; j += 4) {
+    step(PfParity<0>{}, j, s0, s1, n0, n1, rmax);
+    step(PfParity<1>{}, j + 1, n0, n1, s0, s1, rmax);
+    step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
+    step(PfParity<3>{}, j + 3, n0, n1, s0, s1, rmax);
   }
+  if (j < nblk) step(PfParity<0>{}, j, s0, s1, n0, n1, rmax);
+  if (j + 1 < nblk) step(PfParity<1>{}, j + 1, n0, n1, s0, s1, rmax);
+  if (j + 2 < nblk) step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
 
   // ---- normalise and store: lane owns query qi, d = 32 e + 8 (j / 4) + 4 h + j % 4
   const float lt = half_swap_sum(l);
