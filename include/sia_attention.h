@@ -150,6 +150,42 @@ int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_
  * reference's Triton launch allocates nothing (kernels/attention_kernel.py:296). */
 int sia_prefill_workspace_size(int64_t batch, int64_t kv_heads, int64_t kv_len, int64_t head_dim, size_t* bytes);
 
+/* ------------------------------------------------------------ KV write path */
+
+/* Replaces quantize_kv_int8 (model/kv_cache.py:58-67): per-vector symmetric
+ * int8 over head_dim.  amax = max |x| clamped from below by 1e-8 (rounded to
+ * x's dtype), scale = amax / 127 (fp32, correctly rounded), xi = round half
+ * to even of x / scale, clamped to [-127, 127].
+ * x (..., D) f16|bf16|f32 with 1..4 dims, head_dim contiguous and 16-byte
+ * aligned rows; out_int8 same shape int8; out_scale x.shape[:-1] f16 (the
+ * reference's KVCache dtype) or f32 (the paged pools' dtype). */
+int sia_quantize_kv_int8(const sia_tensor* x, const sia_tensor* out_int8, const sia_tensor* out_scale, void* stream);
+
+/* Writes new K/V tokens into a cache.  Replaces the write half of
+ * KVCache.update (model/kv_cache.py:133-184), the decode-step
+ * quantize_kv_int8 + index_copy_ scatter (ops/attention.py:217-228),
+ * PagedKVCache.write_prefill (model/paged_kv_cache.py:89-109) and the
+ * per-step paged write slot_for that the reference documents but does not
+ * implement (model/paged_kv_cache.py:29-30).
+ * k, v (B, H, T, D) f16|bf16|f32 (v may be NULL to write k alone).
+ * Token t of (b, h) goes to position p = start_pos_host + start_pos[b] + t,
+ * with start_pos an int32 device tensor ((1,)/() shared or (B,) per
+ * sequence, read on the device: graph safe) or NULL (then p = start_pos_host
+ * + t, checked against the cache length on the host).
+ *  - block_table NULL: k_dst/v_dst are a contiguous cache (B' >= B, H, S, D)
+ *    (a view into (L, B, H, S, D)); p must be < S.
+ *  - block_table (B, max_blocks) int32: k_dst/v_dst are a paged pool
+ *    (num_pages, H, page_size, D); p goes to page block_table[b][p / page_size]
+ *    at offset p % page_size.
+ * Destination dtype f16|bf16|f32 (value cast) or int8 (quantised exactly as
+ * sia_quantize_kv_int8, with the per-token-per-head scale written to
+ * k_scale_dst / v_scale_dst, shaped like the destination without head_dim,
+ * f16 or f32).  Positions outside the destination (p >= capacity, page id
+ * outside the pool) are skipped on the device, never written. */
+int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_dst, const sia_tensor* v_dst,
+                 const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst, const sia_tensor* block_table,
+                 const sia_tensor* start_pos, int32_t start_pos_host, int32_t page_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -309,3 +309,55 @@ def flash_attention(q, k, v, causal: bool, sm_scale: float | None = None) -> np.
             o = (p @ v[b, h]) / np.where(l == 0.0, 1.0, l)[:, None]
             out[b, hq] = o
     return out
+
+
+# ---------------------------------------------------------------------------
+# KV write path
+# ---------------------------------------------------------------------------
+
+
+def kv_write_positions(B: int, T: int, start, start_offset: int = 0) -> np.ndarray:
+    """Position of token t of sequence b: ``start_offset + start[b] + t`` -> (B, T) int64.
+
+    ``start`` is a scalar or one value per sequence; the reference's writes use
+    ``start_pos`` (``model/kv_cache.py:146,178-179``) and, in the captured
+    decode step, the device position ``ctx.pos_index`` (``ops/attention.py:221-228``).
+    """
+    s = np.asarray(start, dtype=np.int64).reshape(-1)
+    s = np.full(B, int(s[0])) if s.size == 1 else s
+    return start_offset + s[:, None] + np.arange(T)[None, :]
+
+
+def kv_write_contiguous(cache, x, start, start_offset: int = 0):
+    """Store x (B, H, T, ...) into cache (B', H, S, ...) at the positions above; positions
+    outside [0, S) are dropped.  Restates the slice assignment of
+    ``model/kv_cache.py:167-180``.  Returns a new array."""
+    out = np.array(cache, copy=True)
+    B, H, T = x.shape[:3]
+    pos = kv_write_positions(B, T, start, start_offset)
+    for b in range(B):
+        for t in range(T):
+            p = int(pos[b, t])
+            if 0 <= p < out.shape[2]:
+                out[b, :, p] = x[b, :, t]
+    return out
+
+
+def kv_write_paged(pool, x, block_table, page_size: int, start, start_offset: int = 0):
+    """Store x (B, H, T, ...) into pool (num_pages, H, page_size, ...): position p of
+    sequence b goes to page ``block_table[b][p // page_size]``, offset ``p % page_size``
+    (``model/paged_kv_cache.py:89-109``); positions past the table or pages outside
+    the pool are dropped.  Returns a new array."""
+    out = np.array(pool, copy=True)
+    bt = np.asarray(block_table)
+    B, H, T = x.shape[:3]
+    pos = kv_write_positions(B, T, start, start_offset)
+    for b in range(B):
+        for t in range(T):
+            p = int(pos[b, t])
+            if p < 0 or p // page_size >= bt.shape[1]:
+                continue
+            pg = int(bt[b, p // page_size])
+            if 0 <= pg < out.shape[0]:
+                out[pg, :, p % page_size] = x[b, :, t]
+    return out

@@ -24,9 +24,19 @@ from .decode import (
     paged_gqa_int8_flash_decode,
 )
 from .prefill import attention_flash_triton, prefill_workspace_size
+from .kv_cache import KVCache, kv_write, quantize_kv_int8
+from .paged_kv_cache import PagedKVCache
+from .attention import DecodeCtx, decode_step_attention, gqa_attention
 
 __all__ = [
+    "DecodeCtx",
+    "KVCache",
     "LibraryMissing",
+    "PagedKVCache",
+    "decode_step_attention",
+    "gqa_attention",
+    "kv_write",
+    "quantize_kv_int8",
     "attention_flash_triton",
     "SiaError",
     "attention_flash_decode",

@@ -89,6 +89,8 @@ _SIGNATURES = {
                                         ctypes.POINTER(DecodeOptions), _VP],
     "sia_attention_flash_fwd": [_P, _P, _P, _I32, _F, _P, _VP, _SZ, _VP],
     "sia_prefill_workspace_size": [_I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)],
+    "sia_quantize_kv_int8": [_P, _P, _P, _VP],
+    "sia_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _VP],
 }
 _STRING_RESULT = {"sia_status_string", "sia_last_error_message"}
 

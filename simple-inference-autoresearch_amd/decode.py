@@ -82,7 +82,8 @@ def _kv_len_tensor(kv_len, device: torch.device) -> torch.Tensor:
         if kv_len.device != device:
             raise ValueError("kv_len must live on the same device as q")
         return kv_len
-    return torch.tensor([int(kv_len)], dtype=torch.int32, device=device)
+    # a device fill (no host-to-device copy), so the call can still be captured in a graph
+    return torch.full((1,), int(kv_len), dtype=torch.int32, device=device)
 
 
 def _options():

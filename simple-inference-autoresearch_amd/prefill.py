@@ -18,6 +18,7 @@ import torch
 from . import _lib
 
 _HEAD_DIMS = (16, 32, 64, 128, 256)
+_DECODE_DIMS = (64, 128, 256)   # head dims of the decode kernels (single-query calls)
 
 
 @functools.lru_cache(maxsize=256)
@@ -61,6 +62,14 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
     h = _lib.require_library()
     if not q.is_cuda:
         raise ValueError("attention runs on the GPU: q must be a CUDA (HIP) tensor")
+    if Tq == 1 and Tk >= 1 and D in _DECODE_DIMS and k.dtype == q.dtype and v.dtype == q.dtype:
+        # one query row sees every key (bottom-right causal == full at Tq = 1):
+        # the decode kernels stream K/V once per KV-head group instead of
+        # occupying a 256-row prefill work-group per head
+        from .decode import _run
+        kv_len = torch.full((1,), Tk, dtype=torch.int32, device=q.device)
+        out = _run("sia_attention_flash_decode", q, [q, k, v, kv_len], [], Hkv, float(sm_scale))
+        return out if out_token_major else out.view(B, Hq, 1, D)
     q, k, v = (t if _supported_view(t) else t.contiguous() for t in (q, k, v))
     with torch.cuda.device(q.device):
         if out_token_major:

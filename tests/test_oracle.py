@@ -255,3 +255,56 @@ def test_bf16_rounding_helper():
     x = np.array([1.0, 1.00390625, 1.005859375, 1.0078125, -3.14159, 1e-40], dtype=np.float32)
     want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(O.round_to_bf16(x), want)
+
+
+# ------------------------------------------------------------- KV write path
+
+
+def test_paged_write_then_gather_roundtrip():
+    """Writing a sequence into permuted pages and gathering it back by the same table is the identity."""
+    rng = np.random.default_rng(40)
+    B, H, T, D, page = 3, 2, 13, 4, 4
+    nblk = 4
+    x = rng.standard_normal((B, H, T, D))
+    perm = rng.permutation(B * nblk)
+    bt = perm.reshape(B, nblk)
+    pool = O.kv_write_paged(np.zeros((B * nblk, H, page, D)), x, bt, page, 0)
+    for b in range(B):
+        np.testing.assert_array_equal(O.paged_gather(pool, bt, b, T, page), x[b])
+
+
+def test_paged_write_matches_reference_prefill_layout():
+    """Sequential tables (allocate()) put token t of b at block b*nblk + t//page, offset t%page:
+    the full-block reshape-copy of model/paged_kv_cache.py:97-104, written here with numpy
+    reshapes.  (The reference's ragged-tail copy, lines 105-108, transposes (H, tail, D) to
+    (tail, H, D) before assigning into (H, tail, D); the layout its docstring states -- token t
+    at offset t % page for every head -- is what is pinned here.)"""
+    rng = np.random.default_rng(41)
+    B, H, T, D, page, nblk = 2, 3, 10, 2, 4, 3
+    x = rng.standard_normal((B, H, T, D))
+    bt = np.arange(B * nblk).reshape(B, nblk)
+    got = O.kv_write_paged(np.zeros((B * nblk, H, page, D)), x, bt, page, 0)
+    want = np.zeros((B * nblk, H, page, D))
+    full = (T // page) * page
+    for b in range(B):
+        base = b * nblk
+        want[base:base + full // page] = x[b, :, :full].reshape(H, full // page, page, D).transpose(1, 0, 2, 3)
+        want[base + full // page, :, :T - full] = x[b, :, full:]
+    np.testing.assert_array_equal(got, want)
+
+
+def test_decode_write_positions_and_bounds():
+    """Per-sequence decode positions (seq_lens - 1) land in the right slots; out-of-range ones drop."""
+    B, H, D, page = 3, 1, 2, 4
+    x = np.arange(B * H * D, dtype=np.float64).reshape(B, H, 1, D) + 1
+    bt = np.array([[2, 0], [1, 3], [5, 4]])
+    seq_lens = np.array([3, 9, 6])           # token being decoded sits at seq_lens - 1
+    pool = O.kv_write_paged(np.zeros((6, H, page, D)), x, bt, page, seq_lens, start_offset=-1)
+    np.testing.assert_array_equal(pool[2, :, 2], x[0, :, 0])    # p=2 -> page bt[0][0]=2, slot 2
+    np.testing.assert_array_equal(pool[4, :, 1], x[2, :, 0])    # p=5 -> page bt[2][1]=4, slot 1
+    # p=8 -> logical block 2, past the 2-block table: dropped
+    assert pool.sum() == x[0].sum() + x[2].sum()
+    cache = O.kv_write_contiguous(np.zeros((B, H, 5, D)), x, [4, 5, 0])
+    np.testing.assert_array_equal(cache[0, :, 4], x[0, :, 0])
+    assert not cache[1].any()                                   # position 5 >= S = 5 is dropped
+    np.testing.assert_array_equal(cache[2, :, 0], x[2, :, 0])
