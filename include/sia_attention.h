@@ -137,7 +137,8 @@ int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_poo
  * 16-byte aligned rows; out (B,Hq,Tq,D) view in q's dtype -- a transposed
  * view of a (B,Tq,Hq,D) buffer gives the reference's out_token_major layout.
  * causal != 0 applies the bottom-right mask: row i sees keys <= (Tk-Tq)+i;
- * rows that see no key are written as zeros.  head_dim 64 or 128.
+ * rows that see no key are written as zeros.  head_dim 16, 32, 64, 128 or 256
+ * (the reference's assert set, kernels/attention_kernel.py:273).
  * workspace: device memory of at least sia_prefill_workspace_size bytes
  * (256-byte aligned); it holds V converted to f16 in the kernel's block
  * layout and is free again when the stream passes the call. */

@@ -19,10 +19,13 @@ int check4(const sia_tensor* t, const char* name) {
   return SIA_OK;
 }
 
-// V^T block images: one f16 (64 x head_dim) image per 64-key block of every (b, kv head).
+bool head_dim_ok(int64_t D) { return D == 16 || D == 32 || D == 64 || D == 128 || D == 256; }
+
+// V^T block images: one f16 (64 x max(head_dim, 32)) image per 64-key block of every (b, kv head).
 int64_t image_bytes(int64_t B, int64_t Hkv, int64_t Tk, int64_t D) {
   const int64_t nkb = (Tk + kPfBN - 1) / kPfBN;
-  return B * Hkv * nkb * kPfBN * D * 2;
+  const int64_t DV = D < 32 ? 32 : D;
+  return B * Hkv * nkb * kPfBN * DV * 2;
 }
 
 }  // namespace
@@ -31,8 +34,9 @@ extern "C" int sia_prefill_workspace_size(int64_t batch, int64_t kv_heads, int64
                                           size_t* bytes) {
   if (bytes == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "bytes is NULL");
   if (batch <= 0 || kv_heads <= 0 || kv_len < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "bad sizes");
-  if (head_dim != 64 && head_dim != 128)
-    return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (64, 128)", (long long)head_dim);
+  if (!head_dim_ok(head_dim))
+    return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (16, 32, 64, 128, 256)",
+                (long long)head_dim);
   *bytes = (size_t)image_bytes(batch, kv_heads, kv_len, head_dim);
   return SIA_OK;
 }
@@ -55,7 +59,8 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
     return fail(SIA_ERR_INVALID_ARGUMENT, "out must be a (B, Hq, Tq, D) view");
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Tq < 0 || Tk < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "bad sizes");
   if (Hq % Hkv) return fail(SIA_ERR_INVALID_ARGUMENT, "Hq must be a multiple of Hkv");
-  if (D != 64 && D != 128) return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (64, 128)", (long long)D);
+  if (!head_dim_ok(D))
+    return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (16, 32, 64, 128, 256)", (long long)D);
   if (Tq > (1 << 30) || Tk > (1 << 30)) return fail(SIA_ERR_UNSUPPORTED, "sequence too long");
   // K rows are fetched by 32-bit buffer offsets of up to 64 rows from a block start
   const int64_t k_sn = bstride(k, 2);
@@ -82,7 +87,8 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.Tq = (int)Tq; a.Tk = (int)Tk;
   a.causal = causal != 0;
   a.qk_scale = sm_scale * 1.4426950408889634f;
-  a.nqblk = (int)((Tq + kPfBM - 1) / kPfBM);
+  const int bm = pf_rows_per_group((int)D);
+  a.nqblk = (int)((Tq + bm - 1) / bm);
   a.nkb = (int)((Tk + kPfBN - 1) / kPfBN);
   const int64_t groups = (int64_t)a.nqblk * B * Hkv;   // work-groups come in runs of G sharing a KV head
   if (groups * a.G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "grid too large");
@@ -93,7 +99,7 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   p.vimg = (char*)workspace;
   p.Hkv = (int)Hkv; p.Tk = (int)Tk; p.nkb = a.nkb;
   p.nblocks = B * Hkv * a.nkb;
-  if (p.nblocks * D / 256 + 1 > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "K/V too large");
+  if (p.nblocks * (D < 32 ? 32 : D) / 256 + 1 > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "K/V too large");
   L.D = (int)D;
   L.dtype = q->dtype;
   L.stream = (hipStream_t)stream;

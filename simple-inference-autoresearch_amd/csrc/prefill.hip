@@ -8,12 +8,12 @@ namespace sia {
 template <int D, class T>
 static int launch_prefill_typed(PrefillLaunch& L) {
   if (L.pack.nblocks > 0) {
-    const int64_t threads = L.pack.nblocks * D;   // one thread per (image chunk, 8 dims)
+    const int64_t threads = L.pack.nblocks * PfCfg<D>::DV;   // one thread per (image chunk, 8 dims)
     hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, L.stream,
                        L.pack);
   }
   const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
-  hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(kPfWaves * 64), 0, L.stream, L.a);
+  hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(PfCfg<D>::waves * 64), 0, L.stream, L.a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
   return SIA_OK;
@@ -22,9 +22,12 @@ static int launch_prefill_typed(PrefillLaunch& L) {
 int launch_prefill(PrefillLaunch& L) {
   const bool bf = L.dtype == SIA_BF16;
   switch (L.D) {
+    case 16: return bf ? launch_prefill_typed<16, BF16>(L) : launch_prefill_typed<16, F16>(L);
+    case 32: return bf ? launch_prefill_typed<32, BF16>(L) : launch_prefill_typed<32, F16>(L);
     case 64: return bf ? launch_prefill_typed<64, BF16>(L) : launch_prefill_typed<64, F16>(L);
     case 128: return bf ? launch_prefill_typed<128, BF16>(L) : launch_prefill_typed<128, F16>(L);
-    default: return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %d not supported (64, 128)", L.D);
+    case 256: return bf ? launch_prefill_typed<256, BF16>(L) : launch_prefill_typed<256, F16>(L);
+    default: return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %d not supported (16, 32, 64, 128, 256)", L.D);
   }
 }
 

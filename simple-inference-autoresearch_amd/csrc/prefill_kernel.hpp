@@ -72,15 +72,33 @@ struct PackArgs {
   int64_t nblocks;                              // B * Hkv * nkb
 };
 
-constexpr int kPfWaves = 8;             // waves per work-group (two per SIMD)
-constexpr int kPfBM = 32 * kPfWaves;    // query rows per work-group (32 per wave)
 constexpr int kPfBN = 64;               // keys per block
-constexpr int kPfStages = 4;            // K and V LDS ring depth: three blocks in flight
 constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (32-bit data, no swizzle)
 
-// Bytes of one K block (64 rows of D) and of one V^T block image.
+// Per-head-dim configuration of prefill_fwd.  Up to D = 128: 8 waves (two per
+// SIMD, 256 VGPRs each), a four-stage K/V ring (three blocks in flight).
+// D = 256: the O^T accumulators alone take 128 registers per lane, so 4 waves
+// run one per SIMD with 512 registers, and the 32 KB blocks fit LDS as a
+// two-stage ring.  The PV product works on 32-dimension tiles, so V images are
+// at least 32 dimensions wide (D = 16 is zero-padded).
 template <int D>
-constexpr int pf_block_bytes() { return kPfBN * D * 2; }
+struct PfCfg {
+  static constexpr int waves = D <= 128 ? 8 : 4;
+  static constexpr int stages = D <= 128 ? 4 : 2;
+  static constexpr int wpe = D <= 128 ? 2 : 1;          // waves per SIMD the registers are budgeted for
+  static constexpr int BM = 32 * waves;                  // query rows per work-group
+  static constexpr int DV = D < 32 ? 32 : D;             // V^T image dimensions
+  static constexpr int kblk = kPfBN * D * 2;             // bytes of one K block
+  static constexpr int vblk = kPfBN * DV * 2;            // bytes of one V^T image
+  static constexpr int kdma = kblk / 1024;               // 1 KB DMA instructions per K block
+  static constexpr int vdma = vblk / 1024;
+  static constexpr int kper = (kdma + waves - 1) / waves;   // per wave (waves past the count issue
+  static constexpr int vper = (vdma + waves - 1) / waves;   // empty transfers into a dummy area)
+  static constexpr bool dummy = kper * waves != kdma || vper * waves != vdma;
+};
+
+// Query rows per work-group of prefill_fwd at head_dim D (host side).
+inline int pf_rows_per_group(int D) { return D <= 128 ? 256 : 128; }
 
 // Key (0..63 within its block) held by element i (0..7) of image chunk c: the
 // keys of 16-key group c/2 in the order of the S^T output registers of lanes
@@ -99,11 +117,13 @@ __device__ __forceinline__ uint32_t to_f16_pair(BF16, uint32_t a, uint32_t b, in
 }
 
 // V (B, Hkv, Tk, D) -> images [B][Hkv][nkb]: image chunk c of dimension d
-// (16 bytes at (c * D + d) * 16) holds keys image_key(c, 0..7) of d as f16;
-// keys at or past Tk are zero.  One thread makes 8 (d) x 8 (keys).
+// (16 bytes at (c * DV + d) * 16) holds keys image_key(c, 0..7) of d as f16;
+// keys at or past Tk and dimensions past D are zero.  One thread makes 8 (d)
+// x 8 (keys).
 template <int D, class T>
 __global__ __launch_bounds__(256) void prefill_pack_v(const PackArgs a) {
-  constexpr int DG = D / 8;
+  constexpr int DV = PfCfg<D>::DV;
+  constexpr int DG = DV / 8;
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t blk = gid / (8 * DG);
   if (blk >= a.nblocks) return;
@@ -118,9 +138,9 @@ __global__ __launch_bounds__(256) void prefill_pack_v(const PackArgs a) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int key = kb * kPfBN + image_key(c, i);
-    in[i] = key < a.Tk ? *(const u32x4*)(src + (int64_t)key * a.v_sn) : u32x4{0u, 0u, 0u, 0u};
+    in[i] = key < a.Tk && 8 * dg < D ? *(const u32x4*)(src + (int64_t)key * a.v_sn) : u32x4{0u, 0u, 0u, 0u};
   }
-  char* dst = a.vimg + blk * pf_block_bytes<D>() + (int64_t)(c * D + 8 * dg) * 16;
+  char* dst = a.vimg + blk * PfCfg<D>::vblk + (int64_t)(c * DV + 8 * dg) * 16;
 #pragma unroll
   for (int x = 0; x < 8; ++x) {
     u32x4 w;
@@ -173,26 +193,32 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
 }
 
 template <int D, class T>
-__global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void prefill_fwd(const PrefillArgs a) {
+__global__ __launch_bounds__(PfCfg<D>::waves * 64) __attribute__((amdgpu_waves_per_eu(PfCfg<D>::wpe)))
+void prefill_fwd(const PrefillArgs a) {
+  using C = PfCfg<D>;
+  constexpr int NW = C::waves, S = C::stages, DV = C::DV, BM = C::BM;
   constexpr int KST = D / 16;                   // QK k-steps
-  constexpr int ET = D / 32;                    // O^T d-tiles
-  constexpr int BLK = pf_block_bytes<D>();
-  constexpr int NDMA = BLK / 1024 / kPfWaves;   // 1 KB DMA instructions per wave per tensor and block
-  static_assert(NDMA >= 1 && 2 * NDMA * 2 <= 8, "DMA split");
+  constexpr int ET = DV / 32;                   // O^T d-tiles
+  constexpr int KB = C::kblk, VB = C::vblk;
+  constexpr int NK = C::kper, NV = C::vper;     // DMA instructions per wave per block
+  constexpr int GROUP = NK + NV;                // per DMA group (K of one block, V of another)
+  static_assert(S == 2 || S == 4, "ring depth");
+  static_assert((S - 2) * GROUP <= 15, "vmcnt range");
   // K stages: swizzled row-major (below); V^T image chunk c of dimension d at
   // c * D * 16 + d * 16
   // (distinct arrays per stage: the compiler then sees that a DMA into one
   // stage never aliases the LDS reads of another and adds no waits)
-  __shared__ __attribute__((aligned(1024))) char lk0[BLK], lk1[BLK], lk2[BLK], lk3[BLK];
-  __shared__ __attribute__((aligned(1024))) char lv0[BLK], lv1[BLK], lv2[BLK], lv3[BLK];
-  static_assert(kPfStages == 4, "four stage arrays");
+  __shared__ __attribute__((aligned(1024))) char lk0[KB], lk1[KB], lk2[S > 2 ? KB : 16], lk3[S > 2 ? KB : 16];
+  __shared__ __attribute__((aligned(1024))) char lv0[VB], lv1[VB], lv2[S > 2 ? VB : 16], lv3[S > 2 ? VB : 16];
+  // destination of the empty transfers of waves past a block's DMA count
+  __shared__ __attribute__((aligned(1024))) char ldummy[C::dummy ? 1024 : 16];
   auto kstage = [&](auto s) -> char* {
-    constexpr int S = decltype(s)::value & 3;
-    return S == 0 ? lk0 : S == 1 ? lk1 : S == 2 ? lk2 : lk3;
+    constexpr int I = decltype(s)::value % S;
+    return I == 0 ? lk0 : I == 1 ? lk1 : I == 2 ? lk2 : lk3;
   };
   auto vstage = [&](auto s) -> char* {
-    constexpr int S = decltype(s)::value & 3;
-    return S == 0 ? lv0 : S == 1 ? lv1 : S == 2 ? lv2 : lv3;
+    constexpr int I = decltype(s)::value % S;
+    return I == 0 ? lv0 : I == 1 ? lv1 : I == 2 ? lv2 : lv3;
   };
 
   // ---- block -> (query block, b, hq), heaviest first, KV-head groups per XCD
@@ -213,7 +239,7 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   const int wave = uniform(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
   const int off = a.Tk - a.Tq;                           // bottom-right causal offset
-  const int q0 = qblk * kPfBM;
+  const int q0 = qblk * BM;
   const int qi = q0 + wave * 32 + l32;                   // this lane's query row
 
   // ---- Q^T operand (B of S^T = K Q^T): query qi, d = 16 j + 8 h + [0, 8)
@@ -224,7 +250,7 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     for (int j = 0; j < KST; ++j) qop[j] = qi < a.Tq ? *(const u32x4*)(qp + 32 * j) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  const int kend = a.causal ? min(a.Tk, off + q0 + kPfBM) : a.Tk;
+  const int kend = a.causal ? min(a.Tk, off + q0 + BM) : a.Tk;
   const int nblk = kend > 0 ? (kend + kPfBN - 1) / kPfBN : 0;   // key blocks of the work-group
   const int wrow0 = q0 + wave * 32;                      // this wave's first row
   const int wend = a.causal ? min(a.Tk, off + wrow0 + 32) : a.Tk;   // keys this wave can see
@@ -235,7 +261,7 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   const int lim = a.causal ? min(a.Tk - 1, off + qi) : a.Tk - 1;   // this lane's last visible key
 
   const char* kb = a.k + b * a.k_sb + (int64_t)hkv * a.k_sh;
-  const char* vimg = a.vimg + ((int64_t)b * a.Hkv + hkv) * a.nkb * BLK;
+  const char* vimg = a.vimg + ((int64_t)b * a.Hkv + hkv) * a.nkb * VB;
   // K stages are row-major with an XOR swizzle: 16-byte chunk c of key row r
   // sits in slot c ^ (r % NC) of the row's RB bytes.  A DMA instruction then
   // reads whole rows (16 lanes per 256-byte row at D = 128: coalesced), and
@@ -243,10 +269,10 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   // hit 8 different bank groups.  k_voff[i]: this lane's byte offset inside
   // the block for DMA instruction i of the wave.
   constexpr int RB = 2 * D, NC = D / 8, ROWS_PER_DMA = 1024 / RB;
-  int k_voff[NDMA];
+  int k_voff[NK];
 #pragma unroll
-  for (int i = 0; i < NDMA; ++i) {
-    const int r = (wave * NDMA + i) * ROWS_PER_DMA + lane / NC;
+  for (int i = 0; i < NK; ++i) {
+    const int r = (wave * NK + i) * ROWS_PER_DMA + lane / NC;
     k_voff[i] = r * (int)a.k_sn + (((lane % NC) ^ (r % NC)) * 16);
   }
   // QK operand addresses: k-step j reads chunk 2 j + h of row l32 (tile 0)
@@ -255,36 +281,44 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
   for (int j = 0; j < KST; ++j) k_rd[j] = l32 * RB + (((2 * j + h) ^ (l32 % NC)) * 16);
 
-  // DMA of K block `blk` / V^T image `blk` into its ring stage (blk % 4):
-  // wave w moves chunks [w NDMA, (w+1) NDMA) (64 rows each; rows past Tk read
-  // as zero through the buffer bound) and the same range of 1 KB pieces of
-  // the image.  A block past the work-group's last one is issued with an
-  // empty buffer range: the hardware drops every out-of-range read (no memory
-  // traffic) and the stage it fills is never used, so every DMA group has the
-  // same instruction count and the waits below are constants.
+  // DMA of K block `blk` / V^T image `blk` into its ring stage (blk % S):
+  // wave w moves 1 KB pieces [w NK, (w+1) NK) of the block (rows past Tk
+  // read as zero through the buffer bound) and the same range of the image.
+  // A block past the work-group's last one, and a piece past the block's end
+  // (waves beyond the DMA count at small head_dim), is issued with an empty
+  // buffer range: the hardware drops every out-of-range read (no memory
+  // traffic) and what it fills is never read, so every wave issues the same
+  // instruction count per group and the waits below are constants.
   auto issue_k = [&](int blk, char* LK) {
     const bool live = blk < nblk;
     const int key0 = live ? blk * kPfBN : 0;
     const int rows = live ? min(kPfBN, a.Tk - key0) : 0;
-    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(kb + (int64_t)key0 * a.k_sn), 0, rows * (int)a.k_sn, kBufferFlags);
 #pragma unroll
-    for (int i = 0; i < NDMA; ++i) {
-      const int c = wave * NDMA + i;
-      // (through a local: an array element passed straight to this builtin makes
-      // the host pass drop the kernel's launch stub)
+    for (int i = 0; i < NK; ++i) {
+      const int c = wave * NK + i;
+      const bool real = c < C::kdma;
+      const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(kb + (int64_t)key0 * a.k_sn), 0, real ? rows * (int)a.k_sn : 0, kBufferFlags);
+      // (every argument through a plain local: an expression such as an array
+      // element or a conditional passed straight to this builtin makes the
+      // host compilation pass drop the kernel's launch stub)
       const int voff = k_voff[i];
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, LK + c * 1024, 16, voff, 0, 0, 0);
+      char* dst = real ? LK + c * 1024 : ldummy;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, dst, 16, voff, 0, 0, 0);
     }
   };
   auto issue_v = [&](int blk, char* LV) {
     const bool live = blk < nblk;
-    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-        (void*)(vimg + (live ? (int64_t)blk * BLK : 0)), 0, live ? BLK : 0, kBufferFlags);
 #pragma unroll
-    for (int i = 0; i < NDMA; ++i) {
-      const int c = wave * NDMA + i;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, LV + c * 1024, 16, lane * 16, c * 1024, 0, 0);
+    for (int i = 0; i < NV; ++i) {
+      const int c = wave * NV + i;
+      const bool real = c < C::vdma;
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(vimg + (live ? (int64_t)blk * VB : 0)), 0, live && real ? VB : 0, kBufferFlags);
+      char* dst = real ? LV + c * 1024 : ldummy;
+      const int soff = real ? c * 1024 : 0;
+      const int voff = lane * 16;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, dst, 16, voff, soff, 0, 0);
     }
   };
 
@@ -369,12 +403,12 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   };
   // O^T += V^T P^T: operand chunk 2 ks + h of dimension 32 e + l32
   auto pv = [&](const char* V, const u32x4* pop) {
-    const char* vr = V + h * D * 16 + l32 * 16;
+    const char* vr = V + h * DV * 16 + l32 * 16;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int e = 0; e < ET; ++e) {
-        const u32x4 va = *(const u32x4*)(vr + ks * 2 * D * 16 + e * 512);
+        const u32x4 va = *(const u32x4*)(vr + ks * 2 * DV * 16 + e * 512);
         o[e] = mfma32x32x16(F16{}, va, pop[ks], o[e]);
       }
     }
@@ -384,14 +418,14 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
   // g_x = {K_{x+1}, V_x} (x >= 1); step j consumes g_j (K_{j+1} for the
   // scores of the next block, V_j for this block's PV) and, after the
   // barrier that retires step j - 1, refills the stages of K_j and V_{j-1}
-  // with g_{j+3}, so three groups stay in flight.  Within a step the MFMAs
+  // with g_{j+S-1}, so S - 1 groups stay in flight.  Within a step the MFMAs
   // of S_{j+1} run under the softmax of block j.
   auto step = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1, float& rmax) {
-    wait_vmcnt(4 * NDMA);                                // this wave's part of g_j landed (g_{j+1}, g_{j+2} may fly)
+    wait_vmcnt((S - 2) * GROUP);                         // this wave's part of g_j landed (later groups may fly)
     ring_barrier();                                      // everyone's part landed; step j - 1 retired
-    constexpr int P = decltype(parity)::value;           // j % 4, known at compile time
-    issue_k(j + 4, kstage(PfParity<P>{}));
-    issue_v(j + 3, vstage(PfParity<P + 3>{}));
+    constexpr int P = decltype(parity)::value;           // j % S, known at compile time
+    issue_k(j + S, kstage(PfParity<P>{}));
+    issue_v(j + S - 1, vstage(PfParity<P + S - 1>{}));
     if (j < wblk) {
       raise_max(rmax);
       // S_{j+1} is computed even on the wave's last block (its stage then
@@ -424,11 +458,13 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     issue_k(0, lk0);
     issue_v(0, lv0);
     issue_k(1, lk1);
-    issue_k(2, lk2);
-    issue_v(1, lv1);
-    issue_k(3, lk3);
-    issue_v(2, lv2);
-    wait_vmcnt(4 * NDMA);                                // g_0 landed
+    if constexpr (S > 2) {
+      issue_k(2, lk2);
+      issue_v(1, lv1);
+      issue_k(3, lk3);
+      issue_v(2, lv2);
+    }
+    wait_vmcnt((S - 2) * GROUP);                         // g_0 landed
     ring_barrier();
     if (wblk > 0) {
       qk(lk0, s0, s1);
@@ -436,18 +472,22 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
       rmax = rowmax(s0, s1);
     }
   }
-  // unrolled by four: stage arrays and the roles of the two score tiles are
-  // fixed per step at compile time
+  // unrolled by S (even): stage arrays and the roles of the two score tiles
+  // are fixed per step at compile time
   int j = 0;
-  for (; j + 3 < nblk; j += 4) {
+  for (; j + S - 1 < nblk; j += S) {
     step(PfParity<0>{}, j, s0, s1, n0, n1, rmax);
     step(PfParity<1>{}, j + 1, n0, n1, s0, s1, rmax);
-    step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
-    step(PfParity<3>{}, j + 3, n0, n1, s0, s1, rmax);
+    if constexpr (S > 2) {
+      step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
+      step(PfParity<3>{}, j + 3, n0, n1, s0, s1, rmax);
+    }
   }
   if (j < nblk) step(PfParity<0>{}, j, s0, s1, n0, n1, rmax);
-  if (j + 1 < nblk) step(PfParity<1>{}, j + 1, n0, n1, s0, s1, rmax);
-  if (j + 2 < nblk) step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
+  if constexpr (S > 2) {
+    if (j + 1 < nblk) step(PfParity<1>{}, j + 1, n0, n1, s0, s1, rmax);
+    if (j + 2 < nblk) step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
+  }
 
   // ---- normalise and store: lane owns query qi, d = 32 e + 8 (j / 4) + 4 h + j % 4
   const float lt = half_swap_sum(l);
@@ -458,6 +498,7 @@ __global__ __launch_bounds__(kPfWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     for (int e = 0; e < ET; ++e)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
+        if (32 * e + 8 * g4 >= D) continue;            // zero-padded image dimensions (D = 16)
         u32x2 w;
         w[0] = pack2(T{}, o[e][4 * g4 + 0] * inv, o[e][4 * g4 + 1] * inv);
         w[1] = pack2(T{}, o[e][4 * g4 + 2] * inv, o[e][4 * g4 + 3] * inv);

@@ -48,7 +48,7 @@ def qkv(B, Hq, Hkv, Tq, Tk, D, dtype, seed, scale=0.5):
     return q, k, v
 
 
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("T", [1, 17, 128, 130, 300])
 @pytest.mark.parametrize("causal", [True, False])
@@ -71,6 +71,16 @@ def test_offset_causal(gpu_pkg, Tq, Tk):
     check(out, ref, f"Tq={Tq} Tk={Tk}")
     if Tq > Tk:
         assert torch.all(out[:, :, :Tq - Tk] == 0)
+
+
+@pytest.mark.parametrize("Tq,Tk", [(300, 300), (37, 421), (129, 64)])
+def test_qwen_shape_d256(gpu_pkg, Tq, Tk):
+    """Qwen3.5 full-attention layers: head_dim 256, 16 query / 4 KV heads (model/qwen35_plugin.py)."""
+    announce(f"prefill D=256 Qwen shape Tq={Tq} Tk={Tk}")
+    q, k, v = qkv(1, 16, 4, Tq, Tk, 256, torch.bfloat16, seed=Tq + Tk)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True)
+    torch.cuda.synchronize()
+    check(out.transpose(1, 2), O.flash_attention(f64(q), f64(k), f64(v), True), f"D=256 Tq={Tq} Tk={Tk}")
 
 
 def test_strided_views_and_token_major(gpu_pkg):
