@@ -82,6 +82,7 @@ int sia_decode_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv
                               int64_t head_dim, size_t* bytes);
 
 /* Replaces attention_flash_decode (kernels/flash_decode_kernel.py:119-160).
+ * Every decode entry point takes head_dim 16, 32, 64, 128 or 256.
  * q (B,Hq,1,D) f16|bf16; k,v (B,Hkv,S,D) same dtype as q (views into the cache);
  * kv_len int32 (1,)|()|(B,) on device; out (B,1,Hq,D) dtype of q. */
 int sia_attention_flash_decode(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v,

@@ -68,8 +68,8 @@ int prepare_common(const sia_tensor* q, const sia_tensor* kv_len, const sia_tens
     return fail(SIA_ERR_UNSUPPORTED, "q dtype %s: expected float16 or bfloat16", dtype_name(q->dtype));
   if (q->shape[2] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "decode kernel expects a single query position");
   if ((rc = geometry(q->shape[0], q->shape[1], Hkv, q->shape[3], g))) return rc;
-  if (g.D != 64 && g.D != 128 && g.D != 256)
-    return fail(SIA_ERR_UNSUPPORTED, "unsupported head_dim %d (this build supports 64, 128, 256)", g.D);
+  if (g.D != 16 && g.D != 32 && g.D != 64 && g.D != 128 && g.D != 256)
+    return fail(SIA_ERR_UNSUPPORTED, "unsupported head_dim %d (16, 32, 64, 128, 256)", g.D);
   if (q->stride[3] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "q must be contiguous along head_dim");
   if (!aligned16(q->data) || bstride(q, 0) % 16 || bstride(q, 1) % 16)
     return fail(SIA_ERR_INVALID_ARGUMENT, "q rows must be 16-byte aligned");

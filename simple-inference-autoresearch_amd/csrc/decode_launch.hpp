@@ -56,13 +56,18 @@ int launch_decode_typed(DecodeLaunch& L) {
 template <class KV, class QT, class ST>
 int launch_decode_256(DecodeLaunch& L);
 
+// head_dim 16 and 32 run on a wave-per-row kernel (decode_small.hip).
+template <class KV, class QT, class ST>
+int launch_decode_small(DecodeLaunch& L);
+
 template <class KV, class QT, class ST>
 int launch_decode_d(DecodeLaunch& L) {
   switch (L.D) {
+    case 16: case 32: return launch_decode_small<KV, QT, ST>(L);
     case 64: return launch_decode_typed<64, KV, QT, ST>(L);
     case 128: return launch_decode_typed<128, KV, QT, ST>(L);
     case 256: return launch_decode_256<KV, QT, ST>(L);
-    default: return fail(SIA_ERR_UNSUPPORTED, "head_dim %d not supported (64, 128, 256)", L.D);
+    default: return fail(SIA_ERR_UNSUPPORTED, "head_dim %d not supported (16, 32, 64, 128, 256)", L.D);
   }
 }
 

@@ -68,7 +68,7 @@ def contiguous_case(B, Hq, Hkv, S, D, kv_dtype, q_dtype, seed, scale_dtype=torch
 # ------------------------------------------------------------- contiguous
 
 
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("G", [1, 4, 8])
 def test_contiguous_fp(gpu_pkg, D, dtype, G):
@@ -85,7 +85,7 @@ def test_contiguous_fp(gpu_pkg, D, dtype, G):
 
 @pytest.mark.parametrize("q_dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("scale_dtype", [torch.float32, torch.float16])
-@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("D", [16, 32, 64, 128, 256])
 def test_contiguous_int8(gpu_pkg, q_dtype, scale_dtype, D):
     announce(f"contiguous int8 decode D={D} q={q_dtype} scales={scale_dtype}")
     B, Hq, Hkv, S = 3, 8, 2, 300
@@ -175,6 +175,20 @@ def test_paged_small(gpu_pkg, kv, page):
     torch.cuda.synchronize()
     ref = oracle_paged(case)
     assert_close(out, ref, 2e-3, f"paged {kv} page {page}")
+
+
+@pytest.mark.parametrize("kv", ["fp16", "int8"])
+@pytest.mark.parametrize("D", [16, 32])
+def test_paged_small_head_dims(gpu_pkg, kv, D):
+    """head_dim 16 / 32 (wave-per-row kernel): paged, ragged lengths incl. an empty sequence."""
+    announce(f"paged {kv} D={D}")
+    q_dtype = torch.float16 if kv == "fp16" else torch.bfloat16
+    case = _syn().paged_case([500, 0, 16, 129], Hq=8, Hkv=2, D=D, page=16, seed=21, device=DEV, kv=kv,
+                             q_dtype=q_dtype)
+    out = run_paged(gpu_pkg, case)
+    torch.cuda.synchronize()
+    assert_close(out, oracle_paged(case), 2e-3, f"paged {kv} D={D}")
+    assert torch.all(out[1] == 0)
 
 
 @pytest.mark.parametrize("tps", [0, 8, 12, 16, 40, 64])
