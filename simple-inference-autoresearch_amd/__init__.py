@@ -27,6 +27,7 @@ from .prefill import attention_flash_triton, prefill_workspace_size
 from .kv_cache import KVCache, kv_write, quantize_kv_int8
 from .paged_kv_cache import PagedKVCache
 from .attention import DecodeCtx, decode_step_attention, gqa_attention
+from . import plugins  # noqa: F401  (cache builders, transformers attention hook)
 
 __all__ = [
     "DecodeCtx",
