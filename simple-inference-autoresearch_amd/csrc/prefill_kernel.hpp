@@ -201,9 +201,7 @@ void prefill_fwd(const PrefillArgs a) {
   constexpr int ET = DV / 32;                   // O^T d-tiles
   constexpr int KB = C::kblk, VB = C::vblk;
   constexpr int NK = C::kper, NV = C::vper;     // DMA instructions per wave per block
-  constexpr int GROUP = NK + NV;                // per DMA group (K of one block, V of another)
   static_assert(S == 2 || S == 4, "ring depth");
-  static_assert((S - 2) * GROUP <= 15, "vmcnt range");
   // K stages: swizzled row-major (below); V^T image chunk c of dimension d at
   // c * D * 16 + d * 16
   // (distinct arrays per stage: the compiler then sees that a DMA into one
@@ -414,18 +412,11 @@ void prefill_fwd(const PrefillArgs a) {
     }
   };
 
-  // Software pipeline over key blocks.  DMA group g_0 = {K_0, V_0, K_1},
-  // g_x = {K_{x+1}, V_x} (x >= 1); step j consumes g_j (K_{j+1} for the
-  // scores of the next block, V_j for this block's PV) and, after the
-  // barrier that retires step j - 1, refills the stages of K_j and V_{j-1}
-  // with g_{j+S-1}, so S - 1 groups stay in flight.  Within a step the MFMAs
-  // of S_{j+1} run under the softmax of block j.
-  auto step = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1, float& rmax) {
-    wait_vmcnt((S - 2) * GROUP);                         // this wave's part of g_j landed (later groups may fly)
-    ring_barrier();                                      // everyone's part landed; step j - 1 retired
+  // The work of one key block j (sa = raw scores of block j in, sb = scores
+  // of block j + 1 out): the MFMAs of S_{j+1} run under the softmax of
+  // block j, then the PV MFMAs of block j.
+  auto work = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1, float& rmax) {
     constexpr int P = decltype(parity)::value;           // j % S, known at compile time
-    issue_k(j + S, kstage(PfParity<P>{}));
-    issue_v(j + S - 1, vstage(PfParity<P + S - 1>{}));
     if (j < wblk) {
       raise_max(rmax);
       // S_{j+1} is computed even on the wave's last block (its stage then
@@ -454,39 +445,73 @@ void prefill_fwd(const PrefillArgs a) {
 
   f32x16 s0 = f32x16{}, s1 = f32x16{}, n0 = f32x16{}, n1 = f32x16{};
   float rmax = -INFINITY;
-  if (nblk > 0) {
-    issue_k(0, lk0);
-    issue_v(0, lv0);
-    issue_k(1, lk1);
-    if constexpr (S > 2) {
-      issue_k(2, lk2);
-      issue_v(1, lv1);
-      issue_k(3, lk3);
-      issue_v(2, lv2);
-    }
-    wait_vmcnt((S - 2) * GROUP);                         // g_0 landed
-    ring_barrier();
+  auto first_scores = [&]() {
     if (wblk > 0) {
       qk(lk0, s0, s1);
       if (wfull == 0) mask(s0, s1, 0);
       rmax = rowmax(s0, s1);
     }
-  }
-  // unrolled by S (even): stage arrays and the roles of the two score tiles
-  // are fixed per step at compile time
-  int j = 0;
-  for (; j + S - 1 < nblk; j += S) {
-    step(PfParity<0>{}, j, s0, s1, n0, n1, rmax);
-    step(PfParity<1>{}, j + 1, n0, n1, s0, s1, rmax);
-    if constexpr (S > 2) {
-      step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
-      step(PfParity<3>{}, j + 3, n0, n1, s0, s1, rmax);
+  };
+
+  if constexpr (S == 4) {
+    // Four-stage ring, one barrier per two key blocks.  Block j needs K_{j+1}
+    // (scores of the next block) and V_j.  The barrier before blocks j, j+1
+    // (j even) retires blocks j-2, j-1, then refills the stages they read
+    // with K_{j+3}, K_{j+4}, V_{j+2}, V_{j+3}: two blocks of lead, waited
+    // for (vmcnt(0)) at the next barrier.
+    auto super = [&](auto parity, int j, bool second) {
+      constexpr int P = decltype(parity)::value;          // 0 or 2
+      wait_vmcnt(0);                                      // this wave's DMA of blocks j, j+1 landed
+      ring_barrier();                                     // everyone's landed; blocks j-2, j-1 retired
+      issue_k(j + 3, kstage(PfParity<P + 3>{}));
+      issue_v(j + 2, vstage(PfParity<P + 2>{}));
+      issue_k(j + 4, kstage(PfParity<P>{}));
+      issue_v(j + 3, vstage(PfParity<P + 3>{}));
+      work(PfParity<P>{}, j, s0, s1, n0, n1, rmax);
+      if (second) work(PfParity<P + 1>{}, j + 1, n0, n1, s0, s1, rmax);
+    };
+    if (nblk > 0) {
+      issue_k(0, lk0);
+      issue_v(0, lv0);
+      issue_k(1, lk1);
+      issue_k(2, lk2);
+      issue_v(1, lv1);
+      wait_vmcnt(0);
+      ring_barrier();
+      first_scores();
     }
-  }
-  if (j < nblk) step(PfParity<0>{}, j, s0, s1, n0, n1, rmax);
-  if constexpr (S > 2) {
-    if (j + 1 < nblk) step(PfParity<1>{}, j + 1, n0, n1, s0, s1, rmax);
-    if (j + 2 < nblk) step(PfParity<2>{}, j + 2, s0, s1, n0, n1, rmax);
+    int j = 0;
+    for (; j + 3 < nblk; j += 4) {
+      super(PfParity<0>{}, j, true);
+      super(PfParity<2>{}, j + 2, true);
+    }
+    if (j < nblk) super(PfParity<0>{}, j, j + 1 < nblk);
+    if (j + 2 < nblk) super(PfParity<2>{}, j + 2, false);
+  } else {
+    // Two-stage ring, one barrier per block: the barrier before block j
+    // retires block j - 1 and refills its stages with K_{j+2} and V_{j+1}.
+    auto step = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1) {
+      constexpr int P = decltype(parity)::value;
+      wait_vmcnt(0);                                      // this wave's part of K_{j+1}, V_j landed
+      ring_barrier();
+      issue_k(j + 2, kstage(PfParity<P>{}));
+      issue_v(j + 1, vstage(PfParity<P + 1>{}));
+      work(parity, j, sa0, sa1, sb0, sb1, rmax);
+    };
+    if (nblk > 0) {
+      issue_k(0, lk0);
+      issue_v(0, lv0);
+      issue_k(1, lk1);
+      wait_vmcnt(0);
+      ring_barrier();
+      first_scores();
+    }
+    int j = 0;
+    for (; j + 1 < nblk; j += 2) {
+      step(PfParity<0>{}, j, s0, s1, n0, n1);
+      step(PfParity<1>{}, j + 1, n0, n1, s0, s1);
+    }
+    if (j < nblk) step(PfParity<0>{}, j, s0, s1, n0, n1);
   }
 
   // ---- normalise and store: lane owns query qi, d = 32 e + 8 (j / 4) + 4 h + j % 4
