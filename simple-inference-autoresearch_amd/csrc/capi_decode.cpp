@@ -125,6 +125,10 @@ int prepare_kv(const sia_tensor* k, const sia_tensor* v, const Geometry& g, bool
   DecodeArgs& a = L.a;
   a.k = (const char*)k->data; a.k_s0 = bstride(k, 0); a.k_sh = bstride(k, 1); a.k_sn = bstride(k, 2);
   a.v = (const char*)v->data; a.v_s0 = bstride(v, 0); a.v_sh = bstride(v, 1); a.v_sn = bstride(v, 2);
+  if (a.k_sn > 0x7fffffff || a.v_sn > 0x7fffffff || (paged && (a.k_s0 > 0xffffffffLL || a.v_s0 > 0xffffffffLL)))
+    return fail(SIA_ERR_UNSUPPORTED, "k/v token or page stride too large");
+  a.k_tok = (uint32_t)a.k_sn; a.v_tok = (uint32_t)a.v_sn;
+  a.k_pg = paged ? (uint32_t)a.k_s0 : 0u; a.v_pg = paged ? (uint32_t)a.v_s0 : 0u;
   if (paged) {
     if (k->shape[2] != page_size)
       return fail(SIA_ERR_INVALID_ARGUMENT, "k_pool page dim %lld != page_size %d", (long long)k->shape[2], page_size);
@@ -142,7 +146,7 @@ int prepare_kv(const sia_tensor* k, const sia_tensor* v, const Geometry& g, bool
   return SIA_OK;
 }
 
-int prepare_scales(const sia_tensor* ks, const sia_tensor* vs, const sia_tensor* k, DecodeLaunch& L) {
+int prepare_scales(const sia_tensor* ks, const sia_tensor* vs, const sia_tensor* k, bool paged, DecodeLaunch& L) {
   int rc;
   if ((rc = check_tensor(ks, "k_scale", 3))) return rc;
   if ((rc = check_tensor(vs, "v_scale", 3))) return rc;
@@ -154,6 +158,14 @@ int prepare_scales(const sia_tensor* ks, const sia_tensor* vs, const sia_tensor*
   DecodeArgs& a = L.a;
   a.ks = (const char*)ks->data; a.ks_s0 = bstride(ks, 0); a.ks_sh = bstride(ks, 1); a.ks_sn = bstride(ks, 2);
   a.vs = (const char*)vs->data; a.vs_s0 = bstride(vs, 0); a.vs_sh = bstride(vs, 1); a.vs_sn = bstride(vs, 2);
+  if (a.ks_sn > 0x7fffffff || a.vs_sn > 0x7fffffff)
+    return fail(SIA_ERR_UNSUPPORTED, "k_scale/v_scale token stride too large");
+  a.ks_tok = (uint32_t)a.ks_sn; a.vs_tok = (uint32_t)a.vs_sn;
+  if (paged) {
+    if (a.ks_s0 > 0xffffffffLL || a.vs_s0 > 0xffffffffLL)
+      return fail(SIA_ERR_UNSUPPORTED, "k_scale/v_scale page stride too large");
+    a.ks_pg = (uint32_t)a.ks_s0; a.vs_pg = (uint32_t)a.vs_s0;
+  }
   L.scale_dtype = ks->dtype;
   a.scale_vec = ks->dtype == SIA_F32 && ks->stride[2] == 1 && vs->stride[2] == 1 && aligned16(ks->data) &&
                 aligned16(vs->data) && bstride(ks, 0) % 16 == 0 && bstride(ks, 1) % 16 == 0 &&
@@ -221,7 +233,7 @@ int decode_any(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, co
   if ((rc = prepare_kv(k, v, g, bt != nullptr, page_size, L))) return rc;
   if (want_int8) {
     if (k->dtype != SIA_I8) return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be int8 for the int8 entry points");
-    if ((rc = prepare_scales(ks, vs, k, L))) return rc;
+    if ((rc = prepare_scales(ks, vs, k, bt != nullptr, L))) return rc;
   } else if (k->dtype != SIA_F16 && k->dtype != SIA_BF16) {
     return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be float16 or bfloat16 (use the int8 entry points for int8)");
   }

@@ -40,8 +40,10 @@ namespace sia {
 
 constexpr int kTile = 16;          // tokens per MFMA tile
 // Plan header in the workspace (ints): split size, item count, unit blocks per
-// (sequence, split), the work counter; the item prefix per sequence follows.
-constexpr int kPlanTps = 0, kPlanTotal = 1, kPlanUB = 2, kPlanCounter = 3, kPlanHeader = 4;
+// (sequence, split), a pad, the 64-bit work counter (ints 4-5: call epoch in
+// the high half, items handed out in the low half); the item prefix per
+// sequence follows.
+constexpr int kPlanTps = 0, kPlanTotal = 1, kPlanUB = 2, kPlanCounter = 4, kPlanHeader = 6;
 constexpr int kTpsMin = 8;         // smallest split, in tiles
 // The running max is only raised when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^8: well inside f16/bf16 range, and the
@@ -66,6 +68,12 @@ struct DecodeArgs {
   int32_t tps_force;
   int32_t slots;                                     // persistent work-groups of decode_main
   int32_t scale_vec;                                 // scale rows allow 16-byte vector loads
+  uint32_t epoch;                                    // nonzero id of this call (tags the work counter)
+  // 32-bit copies of the per-tile strides (bytes): page strides (0 when
+  // contiguous) and token strides, so the tile address needs only 32x32->64
+  // products
+  uint32_t k_pg, v_pg, ks_pg, vs_pg;
+  uint32_t k_tok, v_tok, ks_tok, vs_tok;
 };
 
 // --------------------------------------------------------------------- plan
@@ -99,16 +107,29 @@ __device__ __forceinline__ void block_sum_max(long long& sum, int& mx, int* red)
   sum = t; mx = m;
 }
 
+// ceil(n / t) for 0 <= n < 2^31, t >= 1, given rt = 1.0 / t in double
+// precision: the product is within one of n / t, and one correction step
+// each way makes the floor exact (integer division is a long instruction
+// sequence on the GPU).
+__device__ __forceinline__ int ceil_div(int n, int t, double rt) {
+  int q = (int)((double)n * rt);
+  int r = n - q * t;
+  q += (r >= t) - (r < 0);
+  r = n - q * t;
+  return q + (r > 0);
+}
+
 // Exclusive scan of cnt[0..B) into pre[0..B] (pre[B] = total), in LDS.
 template <int NW>
 __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pre, int* red, int UB) {
   const int T = NW * 64, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (a.B + T - 1) / T;
   const int b0 = tid * per;
+  const double rt = 1.0 / tps;
   int local = 0;
   for (int i = 0; i < per; ++i) {
     int b = b0 + i;
-    if (b < a.B) local += ((pre[b] + tps - 1) / tps) * UB;
+    if (b < a.B) local += ceil_div(pre[b], tps, rt) * UB;
   }
   int incl = local;
 #pragma unroll
@@ -127,7 +148,7 @@ __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pr
     if (b < a.B) {
       const int cnt = pre[b];
       pre[b] = run;
-      run += ((cnt + tps - 1) / tps) * UB;
+      run += ceil_div(cnt, tps, rt) * UB;
     }
   }
   if (tid == T - 1) pre[a.B] = run;
@@ -143,11 +164,47 @@ __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pr
 // candidate wins (ties go to the larger split, i.e. fewer partials).  With
 // equal lengths this finds the exact balance; with ragged lengths it keeps
 // the heaviest slot close to the mean.
+constexpr int kItemOverhead = 8;   // per-item fixed cost of the split planner, in tiles
+
+// The planner's choice when every sequence has the same length (n tiles):
+// lane c of each wave scores c+1 splits and the wave takes the arg-min, so
+// each wave reaches the same answer with no block-wide step.  Returns 0 when
+// no candidate fits the partial workspace.
+__device__ __forceinline__ int plan_uniform(const DecodeArgs& a, int n, int quantum, int UB, int slots) {
+  const int c = (threadIdx.x & 63) + 1;
+  int t = ceil_div(n, c, 1.0 / c);
+  t = max(t, kTpsMin);
+  t = (t + quantum - 1) / quantum * quantum;
+  const long long items = (long long)a.B * ceil_div(n, t, 1.0 / t) * UB;
+  constexpr long long kInf = (1LL << 36) - 1;
+  long long cost = kInf;
+  if (items <= a.max_items) cost = min(kInf, (long long)ceil_div((int)items, slots, 1.0 / slots) * (t + kItemOverhead));
+  unsigned long long k = ((unsigned long long)cost << 27) | (unsigned long long)(0x7ffffff - t);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long y = __shfl_xor(k, o);
+    k = y < k ? y : k;
+  }
+  if ((long long)(k >> 27) >= kInf) return 0;
+  return uniform(0x7ffffff - (int)(k & 0x7ffffffULL));
+}
+
 template <int NW>
 __device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out, int quantum, int UB, int slots) {
   const int T = NW * 64;
   // quantum: every wave sharing a unit gets the same number of tiles
-  constexpr int kItemOverhead = 8;   // per-item fixed cost, in tiles
+  if (!a.kv_per_seq && a.tps_force <= 0) {
+    // one length for the whole batch: closed form, item prefix b * per
+    const int n = uniform(seq_tiles(a, 0));
+    const int tps = plan_uniform(a, n, quantum, UB, slots);
+    if (tps > 0) {
+      const int per = ceil_div(n, tps, 1.0 / tps) * UB;
+      for (int b = threadIdx.x; b <= a.B; b += T) pre[b] = b * per;
+      __syncthreads();
+      tps_out = tps;
+      return a.B * per;
+    }
+  }
   // lengths (in tiles) into pre[] temporarily, and the longest
   int mx = 0;
   for (int b = threadIdx.x; b < a.B; b += T) {
@@ -158,6 +215,7 @@ __device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out,
   long long dummy = 0;
   block_sum_max<NW>(dummy, mx, red);
   int tps;
+  bool fits = false;   // the chosen split is known to fit the partial workspace
   if (a.tps_force > 0) {
     tps = a.tps_force;
   } else {
@@ -165,18 +223,25 @@ __device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out,
     // threads of a candidate sum the item counts of every 8th sequence
     static_assert(NW * 64 >= 8, "need at least 8 threads");
     const int c = threadIdx.x / 8 + 1, j = threadIdx.x & 7;
-    int t = (mx + c - 1) / c;
+    int t = ceil_div(mx, c, 1.0 / c);
     t = max(t, kTpsMin);
     t = (t + quantum - 1) / quantum * quantum;
-    long long items = 0;
-    for (int b = j; b < a.B; b += 8) items += (pre[b] + t - 1) / t;
-    items += __shfl_xor(items, 1);
-    items += __shfl_xor(items, 2);
-    items += __shfl_xor(items, 4);
-    items *= UB;
+    const double rt = 1.0 / t;
+    // item counts saturate just above the workspace capacity (such a split is out)
+    const int sat = min(a.max_items / UB, 0x7ffffffe) + 1;
+    auto sadd = [sat](int x, int y) { return y >= sat - x ? sat : x + y; };   // x, y in [0, sat]
+    int items = 0;
+    for (int b = j; b < a.B; b += 8) items = sadd(items, ceil_div(pre[b], t, rt));
+    items = sadd(items, __shfl_xor(items, 1));
+    items = sadd(items, __shfl_xor(items, 2));
+    items = sadd(items, __shfl_xor(items, 4));
     constexpr long long kInf = (1LL << 36) - 1;
-    long long cost = (items + slots - 1) / slots * (long long)(t + kItemOverhead);
-    if (items > a.max_items || cost > kInf) cost = kInf;
+    long long cost = kInf;
+    if (items < sat) {
+      const long long all = (long long)items * UB;
+      cost = (long long)ceil_div((int)min(all, (long long)0x7fffffff), slots, 1.0 / slots) * (t + kItemOverhead);
+      if (all > a.max_items || cost > kInf) cost = kInf;
+    }
     // arg-min over the block of (cost, -t): ties prefer the larger split
     unsigned long long k = ((unsigned long long)cost << 27) | (unsigned long long)(0x7ffffff - t);
 #pragma unroll
@@ -192,13 +257,15 @@ __device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out,
 #pragma unroll
     for (int w = 1; w < NW; ++w) best = red64[w] < best ? red64[w] : best;
     tps = 0x7ffffff - (int)(best & 0x7ffffffULL);
+    fits = (long long)(best >> 27) < kInf;
   }
   tps = max(tps, kTpsMin);
   tps = (tps + quantum - 1) / quantum * quantum;
   // Grow the split until the partial workspace can hold every item.
-  for (int guard = 0; guard < 32; ++guard) {
+  for (int guard = 0; guard < 32 && !fits; ++guard) {
     long long items = 0;
-    for (int b = threadIdx.x; b < a.B; b += T) items += (long long)((pre[b] + tps - 1) / tps) * UB;
+    const double rt = 1.0 / tps;
+    for (int b = threadIdx.x; b < a.B; b += T) items += (long long)ceil_div(pre[b], tps, rt) * UB;
     int dm = 0;
     block_sum_max<NW>(items, dm, red);
     if (items <= a.max_items) break;
@@ -223,49 +290,89 @@ struct Tile {
   float ks[4], vs[4];                                // int8 scales of tokens 4*grp + i
 };
 
-// Byte offsets of this lane's operands inside one tile (constant per item).
+// This lane's byte offsets inside one tile (constant): K of token lane16,
+// elements [grp*D/4, +D/4); V of token 4*grp+i, elements [lane16*D/16,
+// +D/16); the scales of tokens 4*grp .. 4*grp+3.
 struct LaneOff {
-  uint32_t k;       // token lane16, elements [grp*D/4, +D/4)
-  uint32_t v[4];    // token 4*grp+i, elements [lane16*D/16, +D/16)
-  uint32_t ks, vs;  // scales of tokens 4*grp .. 4*grp+3
+  uint32_t k;
+  uint32_t v[4];
+  uint32_t ks, vs;
 };
 
-// Uniform base pointers of one tile (scalar registers).
+// Uniform base addresses of one tile.  Tiles are read with buffer loads: a
+// scalar descriptor per tile plus the constant per-lane offsets, so no
+// per-tile vector address arithmetic (and no 64-bit address registers).
 struct TilePtr {
   const char* k; const char* v; const char* ks; const char* vs;
 };
+
+constexpr int kRawBufferFlags = 0x00020000;   // gfx9 raw buffer descriptor word 3 (32-bit data, no swizzle)
+constexpr int kLoadNT = 2;                     // buffer-load cache policy: non-temporal (read once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* p) {
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, -1, kRawBufferFlags);
+}
+
+// BYTES at rsrc + off (BYTES a multiple of 16, or 8 or 4).
+template <int BYTES>
+__device__ __forceinline__ void load_raw_buf(Raw<BYTES>& r, __amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  if constexpr (BYTES % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < BYTES / 16; ++i) {
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, kLoadNT);
+      r.w[4 * i + 0] = x[0]; r.w[4 * i + 1] = x[1]; r.w[4 * i + 2] = x[2]; r.w[4 * i + 3] = x[3];
+    }
+  } else if constexpr (BYTES == 8) {
+    const u32x2 x = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, kLoadNT);
+    r.w[0] = x[0]; r.w[1] = x[1];
+  } else {
+    static_assert(BYTES == 4, "tile operand size");
+    r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, kLoadNT);
+  }
+}
 
 template <class ST>
 __device__ __forceinline__ float load_scale(const char* p) {
   if constexpr (std::is_same<ST, F32>::value) return *(const float*)p;
   else return (float)*(const _Float16*)p;
 }
+template <class ST>
+__device__ __forceinline__ float load_scale(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  if constexpr (std::is_same<ST, F32>::value) return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, kLoadNT));
+  else return (float)__builtin_bit_cast(_Float16, (unsigned short)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, kLoadNT));
+}
 
 // Load this lane's operands of one tile.  FULL: all 16 tokens exist, so no
-// per-lane predicate; otherwise tokens >= `valid` read as zero.
-template <int D, class KV, class ST, bool FULL>
+// per-lane predicate; otherwise tokens >= `valid` read as zero.  SV: the
+// int8 scales of a head are contiguous fp32 rows (one 16-byte load per lane);
+// a compile-time choice, so that the tile loop holds no branch around loads
+// (a branch there makes the compiler wait for the next tile's loads as well).
+template <int D, class KV, class ST, bool FULL, bool SV>
 __device__ __forceinline__ void load_tile(const DecodeArgs& a, const TilePtr& t, const LaneOff& o, int valid,
                                           Tile<D, KV, ST>& c, int lane16, int grp) {
   using C = Tile<D, KV, ST>;
-  if (FULL || lane16 < valid) load_raw<C::KB>(c.k, t.k + o.k);
+  const __amdgpu_buffer_rsrc_t rk = tile_rsrc(t.k), rv = tile_rsrc(t.v);
+  if (FULL || lane16 < valid) load_raw_buf<C::KB>(c.k, rk, o.k);
   else zero_raw<C::KB>(c.k);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if (FULL || 4 * grp + i < valid) load_raw<C::VB>(c.v[i], t.v + o.v[i]);
+    if (FULL || 4 * grp + i < valid) load_raw_buf<C::VB>(c.v[i], rv, o.v[i]);
     else zero_raw<C::VB>(c.v[i]);
   }
   if constexpr (C::kInt8) {
-    if (FULL && std::is_same<ST, F32>::value && a.scale_vec) {
-      const f32x4 k4 = __builtin_nontemporal_load((const f32x4*)(t.ks + o.ks));
-      const f32x4 v4 = __builtin_nontemporal_load((const f32x4*)(t.vs + o.vs));
+    const __amdgpu_buffer_rsrc_t rks = tile_rsrc(t.ks), rvs = tile_rsrc(t.vs);
+    if constexpr (FULL && SV) {
+      static_assert(std::is_same<ST, F32>::value, "vector scale loads are fp32");
+      const u32x4 k4 = __builtin_amdgcn_raw_buffer_load_b128(rks, o.ks, 0, kLoadNT);
+      const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(rvs, o.vs, 0, kLoadNT);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { c.ks[i] = k4[i]; c.vs[i] = v4[i]; }
+      for (int i = 0; i < 4; ++i) { c.ks[i] = __uint_as_float(k4[i]); c.vs[i] = __uint_as_float(v4[i]); }
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool ok = FULL || 4 * grp + i < valid;
-        c.ks[i] = ok ? load_scale<ST>(t.ks + o.ks + i * (uint32_t)a.ks_sn) : 0.0f;
-        c.vs[i] = ok ? load_scale<ST>(t.vs + o.vs + i * (uint32_t)a.vs_sn) : 0.0f;
+        c.ks[i] = ok ? load_scale<ST>(rks, o.ks + i * a.ks_tok) : 0.0f;
+        c.vs[i] = ok ? load_scale<ST>(rvs, o.vs + i * a.vs_tok) : 0.0f;
       }
     }
   }
@@ -336,20 +443,33 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
   constexpr int E = D / 16;
   constexpr bool kInt8 = std::is_same<KV, I8>::value;
 
-  f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int j = 0; j < KSTEPS; ++j) {
-    const u32x4 ka = k_operand<D, KV, ST>(c, j);
-    sacc = mfma16x16x32(MT{}, ka, qop[j], sacc);
-    if constexpr (QSplit<KV, QT>::value) sacc = mfma16x16x32(MT{}, ka, qop_lo[j], sacc);
-  }
   float s[4];
+  if constexpr (kInt8) {
+    // int8 K against the int8 query halves (q = step * (hi + lo/254)):
+    // exact integer dot products, no conversion of K
+    i32x4 shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s[i] = sacc[i] * qmul;
-    if constexpr (kInt8) s[i] *= c.ks[i];
-    if (!FULL && tile * kTile + 4 * grp + i >= ntok) s[i] = -INFINITY;
+    for (int j = 0; j < D / 64; ++j) {
+      const u32x4 ka = {c.k.w[4 * j], c.k.w[4 * j + 1], c.k.w[4 * j + 2], c.k.w[4 * j + 3]};
+      shi = mfma16x16x64_i8(ka, qop[j], shi);
+      slo = mfma16x16x64_i8(ka, qop_lo[j], slo);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = (float)(__mul24(shi[i], 254) + slo[i]) * (qmul * c.ks[i]);
+  } else {
+    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      const u32x4 ka = k_operand<D, KV, ST>(c, j);
+      sacc = mfma16x16x32(MT{}, ka, qop[j], sacc);
+      if constexpr (QSplit<KV, QT>::value) sacc = mfma16x16x32(MT{}, ka, qop_lo[j], sacc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s[i] = sacc[i] * qmul;
   }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (!FULL && tile * kTile + 4 * grp + i >= ntok) s[i] = -INFINITY;
   // Lazy max: the cross-lane reduction and the rescale of (l, acc) run only
   // when some score of this wave exceeds its head's running max.
   const float lmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
@@ -401,20 +521,32 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
   }
 }
 
-// Q operand for a unit: head col c (lane16), element range of group grp.
-// Returns the per-lane score multiplier (sm_scale*log2e, times 2^-shift when
-// the query was rescaled to stay inside f16's range).
+// The query row of a unit as loaded: head col c (lane16), elements
+// [grp*D/4, +D/4) as raw 16-bit words (zero for dead columns).
+template <int D>
+struct QRaw {
+  u32x4 w[D / 32];
+};
+template <int D>
+__device__ __forceinline__ QRaw<D> load_q_raw(const DecodeArgs& a, int b, int hq, bool live, int grp) {
+  QRaw<D> r;
+  const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + grp * (D / 4) * 2;
+#pragma unroll
+  for (int w = 0; w < D / 32; ++w) r.w[w] = live ? *(const u32x4*)(qp + 16 * w) : u32x4{0u, 0u, 0u, 0u};
+  return r;
+}
+
+// Q operand for a unit from its raw row.  Returns the per-lane score
+// multiplier (sm_scale*log2e, times the query's scale step).
 template <int D, class KV, class QT>
-__device__ __forceinline__ float load_q(const DecodeArgs& a, int b, int hq, bool live, int grp,
-                                       u32x4* qop, u32x4* qop_lo) {
+__device__ __forceinline__ float prep_q(const DecodeArgs& a, const QRaw<D>& raw, u32x4* qop, u32x4* qop_lo) {
   using MT = typename MmaOf<KV>::T;
   constexpr int KSTEPS = D / 32;
   constexpr int PER = D / 4;
   float qf[PER];
-  const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + grp * PER * 2;
 #pragma unroll
   for (int w = 0; w < PER / 8; ++w) {
-    const u32x4 x = live ? *(const u32x4*)(qp + 16 * w) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 x = raw.w[w];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       qf[8 * w + 2 * i] = lo_f32(QT{}, x[i]);
@@ -422,6 +554,36 @@ __device__ __forceinline__ float load_q(const DecodeArgs& a, int b, int hq, bool
     }
   }
   float mul = a.qk_scale;
+  if constexpr (std::is_same<KV, I8>::value) {
+    // int8 K: the query becomes two int8 vectors, q = step * (hi + lo/254)
+    // with step = max|q| / 127, |hi|, |lo| <= 127 (error <= step/508 per
+    // element).  Byte order follows the lane's elements, as K's bytes do.
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) amax = fmaxf(amax, fabsf(qf[i]));
+    amax = wave_max_xor16_32(amax);
+    const float inv = amax > 0.f ? 127.0f / amax : 0.f;
+    uint32_t hw[PER / 4], lw[PER / 4];
+#pragma unroll
+    for (int w = 0; w < PER / 4; ++w) {
+      uint32_t h4 = 0, l4 = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y = qf[4 * w + i] * inv;
+        const float h = rintf(y);
+        const int lo = (int)rintf((y - h) * 254.0f);
+        h4 |= ((uint32_t)(int)h & 0xffu) << (8 * i);
+        l4 |= ((uint32_t)lo & 0xffu) << (8 * i);
+      }
+      hw[w] = h4; lw[w] = l4;
+    }
+#pragma unroll
+    for (int j = 0; j < D / 64; ++j) {
+      qop[j] = u32x4{hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]};
+      qop_lo[j] = u32x4{lw[4 * j], lw[4 * j + 1], lw[4 * j + 2], lw[4 * j + 3]};
+    }
+    return amax > 0.f ? mul * (amax / (127.0f * 254.0f)) : 0.f;
+  }
   if constexpr (std::is_same<MT, F16>::value) {
     // Scale the query by a power of two so that max|q| lies in [2^13, 2^14):
     // no f16 overflow, and only elements below 2^-28 of the max lose bits.
@@ -472,7 +634,7 @@ __device__ __forceinline__ ItemShape item_shape(int U) {
   return sh;
 }
 
-template <int D, class KV, class QT, class ST, int NW>
+template <int D, class KV, class QT, class ST, int NW, bool SV>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(DecodeWaves<D, KV>::value)))
 void decode_main(const DecodeArgs a) {
   constexpr int E = D / 16;
@@ -486,19 +648,39 @@ void decode_main(const DecodeArgs a) {
   int* pre = red + 2 * NW + 2;
 
   const ItemShape shape = item_shape<NW>(a.U);
-  // the plan (written by decode_plan just before this kernel): split size,
-  // item count and the item prefix per sequence
-  const int tps = uniform(a.ws_plan[kPlanTps]);
-  const int total = uniform(a.ws_plan[kPlanTotal]);
-  for (int i = threadIdx.x; i <= a.B; i += NW * 64) pre[i] = a.ws_plan[kPlanHeader + i];
+  // The split plan, computed by every work-group from the device-side
+  // lengths (the same in every group).  Group 0 publishes it for
+  // decode_reduce and opens this call's work counter.
+  int tps;
+  const int total = plan_items<NW>(a, pre, red, tps, shape.P, a.UB, (int)gridDim.x);
+  unsigned long long* counter = (unsigned long long*)(a.ws_plan + kPlanCounter);
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[kPlanHeader + i] = pre[i];
+    if (threadIdx.x == 0) {
+      a.ws_plan[kPlanTps] = tps;
+      a.ws_plan[kPlanTotal] = total;
+      a.ws_plan[kPlanUB] = a.UB;
+      atomicExch(counter, (unsigned long long)a.epoch << 32);
+    }
+  }
   // Work assignment: group g first takes item g; items past the grid are
-  // handed out by an atomic counter (zeroed by decode_plan), so a group that
-  // finishes early takes more and ragged batches stay balanced.  Only those
-  // late, naturally staggered requests touch the counter: a burst of
-  // same-address atomics from every group at launch costs more than it saves.
+  // handed out by the counter, so a group that finishes early takes more and
+  // ragged batches stay balanced.  A group asks for its second item only when
+  // its first is done (long after group 0 opened the counter), and for each
+  // later one as that item starts.  A count carrying another call's epoch
+  // (the counter not opened yet) reads as "no item": the group stops, and the
+  // groups still running, group 0 among them, take what is left.  An item
+  // handed out twice is computed twice with identical results.
   int* l_item = red;   // LDS slot broadcasting the next item
-  const bool steal = total > (int)gridDim.x;
-  __syncthreads();
+  int* prog = red + 2;   // tiles done per wave (NW ints; read and written without barriers)
+  const uint32_t steal_range = total > (int)gridDim.x ? (uint32_t)(total - (int)gridDim.x) : 0u;
+  const bool steal = steal_range > 0;
+  auto request = [&]() -> int {
+    const unsigned long long old = atomicAdd(counter, 1ull);
+    const uint32_t n = (uint32_t)old;
+    return ((uint32_t)(old >> 32) == a.epoch && n < steal_range) ? (int)gridDim.x + (int)n : total;
+  };
+  bool first = true;
   int next_item = blockIdx.x;
 
   const int lane = threadIdx.x & 63;
@@ -506,19 +688,20 @@ void decode_main(const DecodeArgs a) {
   const int lane16 = lane & 15, grp = lane >> 4;
   using TileT = Tile<D, KV, ST>;
   LaneOff lo;
-  lo.k = (uint32_t)(lane16 * a.k_sn) + (uint32_t)(grp * TileT::KB);
+  lo.k = lane16 * a.k_tok + (uint32_t)(grp * TileT::KB);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lo.v[i] = (uint32_t)((4 * grp + i) * a.v_sn) + (uint32_t)(lane16 * TileT::VB);
-  lo.ks = (uint32_t)(4 * grp * a.ks_sn);
-  lo.vs = (uint32_t)(4 * grp * a.vs_sn);
+  for (int i = 0; i < 4; ++i) lo.v[i] = (4 * grp + i) * a.v_tok + (uint32_t)(lane16 * TileT::VB);
+  lo.ks = 4 * grp * a.ks_tok;
+  lo.vs = 4 * grp * a.vs_tok;
   const int uin = wave / shape.P;        // unit slot of this wave inside an item
   const int phase = wave - uin * shape.P;
 
   while (next_item < total) {
     const int item = uniform(next_item);
-    // request the following item now; its index is only needed at the end
-    int stolen = 0;
-    if (steal && threadIdx.x == 0) stolen = (int)gridDim.x + atomicAdd(&a.ws_plan[kPlanCounter], 1);
+    // request the following item now (after the first); its index is only
+    // needed at the end
+    int stolen = total;
+    if (steal && !first && threadIdx.x == 0) stolen = request();
     // item -> (b, split, unit block): b is the largest index with pre[b] <= item
     int blo = 0, bhi = a.B;
     while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= item) blo = mid; else bhi = mid; }
@@ -543,78 +726,107 @@ void decode_main(const DecodeArgs a) {
     for (int e = 0; e < E; ++e) st.acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     if (wave_live) {
-      u32x4 qop[KSTEPS], qop_lo[KSTEPS];
-      const float qmul = load_q<D, KV, QT>(a, b, hq, live, grp, qop, qop_lo);
-
       // This wave takes tiles t_lo + phase, + P, ...: `nfull` full tiles
       // (double-buffered) and possibly the sequence's partial last tile.
       const int P = shape.P;
       const bool paged = a.bt != nullptr;
       const int t_first = t_lo + phase;
+      // Page ids come from the block-table row of sequence b; a contiguous
+      // cache reads kv_len[0] instead (value ignored, page stride 0).
+      const int32_t* btrow = paged ? a.bt + (int64_t)b * a.bt_sb : a.kv_len;
+      const int64_t bt_step = paged ? a.bt_sl : 0;
+      const int cap_tiles = a.cap_tokens / kTile;
+      auto page_id = [&](int k) {
+        const int t = min(t_first + k * P, cap_tiles - 1);
+        return uniform(btrow[(int64_t)(t >> a.lg_tiles_per_page) * bt_step]);
+      };
+      // The loads that need only the item go out together: the query row
+      // and the first tile's page id (the length is already in flight).
+      const QRaw<D> qraw = load_q_raw<D>(a, b, hq, live, grp);
+      const int pg0 = page_id(0);
       const int t_full = min(t_hi, ntok / kTile);
       const int nfull = t_first < t_full ? (t_full - t_first + P - 1) / P : 0;
       const int nt = t_first < t_hi ? (t_hi - t_first + P - 1) / P : 0;
       const int64_t rowk = paged ? 0 : (int64_t)b * a.k_s0, rowv = paged ? 0 : (int64_t)b * a.v_s0;
       const int64_t rowks = paged ? 0 : (int64_t)b * a.ks_s0, rowvs = paged ? 0 : (int64_t)b * a.vs_s0;
-      const char* kb = a.k + rowk + (int64_t)hkv * a.k_sh;
-      const char* vb = a.v + rowv + (int64_t)hkv * a.v_sh;
-      const char* ksb = a.ks + rowks + (int64_t)hkv * a.ks_sh;
-      const char* vsb = a.vs + rowvs + (int64_t)hkv * a.vs_sh;
-      const int tpp_mask = (1 << a.lg_tiles_per_page) - 1;
+      const char* kb = a.k + (rowk + (int64_t)hkv * a.k_sh);
+      const char* vb = a.v + (rowv + (int64_t)hkv * a.v_sh);
+      const char* ksb = a.ks + (rowks + (int64_t)hkv * a.ks_sh);
+      const char* vsb = a.vs + (rowvs + (int64_t)hkv * a.vs_sh);
+      // Tile t lives at page `phys`, token (t & mask) * 16 of it.  A
+      // contiguous cache is one page of unbounded length (page stride 0), so
+      // both layouts share one branch-free formula.
+      const int tpp_mask = paged ? (1 << a.lg_tiles_per_page) - 1 : 0x7fffffff;
+      const uint32_t npages = paged ? (uint32_t)min(a.num_pages, (int64_t)0x7fffffff) : 1u;
       auto tile_ptr = [&](int t, int phys) {
         TilePtr tp;
-        int64_t ok, ov, oks, ovs;
-        if (paged) {
-          const int off = (t & tpp_mask) * kTile;
-          ok = (int64_t)phys * a.k_s0 + off * a.k_sn;
-          ov = (int64_t)phys * a.v_s0 + off * a.v_sn;
-          oks = (int64_t)phys * a.ks_s0 + off * a.ks_sn;
-          ovs = (int64_t)phys * a.vs_s0 + off * a.vs_sn;
+        const uint32_t pg = (uint32_t)phys < npages ? (uint32_t)phys : 0u;   // never read outside the pool
+        const uint32_t off = (uint32_t)((t & tpp_mask) * kTile);
+        tp.k = kb + uniform64((uint64_t)pg * a.k_pg + (uint64_t)off * a.k_tok);
+        tp.v = vb + uniform64((uint64_t)pg * a.v_pg + (uint64_t)off * a.v_tok);
+        if constexpr (TileT::kInt8) {
+          tp.ks = ksb + uniform64((uint64_t)pg * a.ks_pg + (uint64_t)off * a.ks_tok);
+          tp.vs = vsb + uniform64((uint64_t)pg * a.vs_pg + (uint64_t)off * a.vs_tok);
         } else {
-          ok = (int64_t)t * kTile * a.k_sn;
-          ov = (int64_t)t * kTile * a.v_sn;
-          oks = (int64_t)t * kTile * a.ks_sn;
-          ovs = (int64_t)t * kTile * a.vs_sn;
+          tp.ks = tp.vs = nullptr;
         }
-        tp.k = kb + ok; tp.v = vb + ov; tp.ks = ksb + oks; tp.vs = vsb + ovs;
         return tp;
       };
-      // page ids of this wave's tiles [w0, w0 + 64) in lanes 0..63
-      auto page_ids = [&](int w0, int wn) {
-        int pg = 0;
-        if (paged && lane < wn) {
-          const int t = t_first + (w0 + lane) * P;
-          pg = a.bt[(int64_t)b * a.bt_sb + (int64_t)(t >> a.lg_tiles_per_page) * a.bt_sl];
-          pg = ((unsigned)pg < (unsigned long long)a.num_pages) ? pg : 0;   // never read outside the pool
-        }
-        return pg;
-      };
-      TileT bufA, bufB;
-      for (int w0 = 0; w0 < nfull; w0 += 64) {
-        const int wn = min(64, nfull - w0);
-        const int pg = page_ids(w0, wn);
+      u32x4 qop[KSTEPS], qop_lo[KSTEPS];
+      float qmul = 0.f;
+      // Full tiles, double-buffered.  The steady-state loop always issues the
+      // next tiles' loads, and fetches the page ids of the tiles two ahead
+      // with one vector load (lanes 0 and 1; indices clamped to the last full
+      // tile), so every load retires in order and computing tile k waits only
+      // for tile k.
+      if (nfull > 0) {
+        const int klast = nfull - 1;
+        auto page_pair = [&](int k0) {
+          const int k = min(k0 + (lane & 1), klast);
+          const int t = t_first + k * P;
+          return btrow[(int64_t)(t >> a.lg_tiles_per_page) * bt_step];
+        };
+        TileT bufA, bufB;
+        // same load order as the loop below (page ids, then a tile), so the
+        // wait counts where the two paths meet stay exact
+        int pgv = page_pair(1);   // tiles k + 1, k + 2
+        load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first, pg0), lo, 16, bufA, lane16, grp);
+        // the query's conversion overlaps the first tile's flight
+        qmul = prep_q<D, KV, QT>(a, qraw, qop, qop_lo);
         int k = 0;
-        load_tile<D, KV, ST, true>(a, tile_ptr(t_first + w0 * P, __builtin_amdgcn_readlane(pg, 0)), lo, 16,
-                                   bufA, lane16, grp);
-        while (true) {
-          if (k + 1 < wn)
-            load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * P, __builtin_amdgcn_readlane(pg, k + 1)),
-                                       lo, 16, bufB, lane16, grp);
+        for (; k + 2 < nfull; k += 2) {
+          // Waves w and w^4 share a SIMD, where the older one wins issue
+          // ties and would finish well ahead: the one that is behind (by
+          // tile count, published in LDS) takes the higher priority.
+          __hip_atomic_store(&prog[wave], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);   // every lane, same value
+          if (k > uniform(__hip_atomic_load(&prog[wave ^ 4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)))
+            __builtin_amdgcn_s_setprio(0);
+          else
+            __builtin_amdgcn_s_setprio(1);
+          const int pg1 = __builtin_amdgcn_readlane(pgv, 0), pg2 = __builtin_amdgcn_readlane(pgv, 1);
+          load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first + (k + 1) * P, pg1), lo, 16, bufB, lane16, grp);
+          pgv = page_pair(k + 3);
           compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, 0, ntok, grp, st);
-          if (++k >= wn) break;
-          if (k + 1 < wn)
-            load_tile<D, KV, ST, true>(a, tile_ptr(t_first + (w0 + k + 1) * P, __builtin_amdgcn_readlane(pg, k + 1)),
-                                       lo, 16, bufA, lane16, grp);
+          load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first + (k + 2) * P, pg2), lo, 16, bufA, lane16, grp);
           compute_tile<D, KV, QT, ST, true>(bufB, qop, qop_lo, qmul, 0, ntok, grp, st);
-          if (++k >= wn) break;
+        }
+        __builtin_amdgcn_s_setprio(0);
+        __hip_atomic_store(&prog[wave], 1 << 30, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (k + 1 < nfull) {
+          load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first + (k + 1) * P, __builtin_amdgcn_readlane(pgv, 0)), lo,
+                                         16, bufB, lane16, grp);
+          compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, 0, ntok, grp, st);
+          compute_tile<D, KV, QT, ST, true>(bufB, qop, qop_lo, qmul, 0, ntok, grp, st);
+        } else {
+          compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, 0, ntok, grp, st);
         }
       }
+      if (nfull == 0) qmul = prep_q<D, KV, QT>(a, qraw, qop, qop_lo);
       if (nt > nfull) {  // the sequence's partial last tile belongs to this wave
         const int t = t_first + nfull * P;
-        const int pg = page_ids(nfull, 1);
-        load_tile<D, KV, ST, false>(a, tile_ptr(t, __builtin_amdgcn_readlane(pg, 0)), lo, ntok - t * kTile,
-                                    bufA, lane16, grp);
-        compute_tile<D, KV, QT, ST, false>(bufA, qop, qop_lo, qmul, t, ntok, grp, st);
+        TileT last;
+        load_tile<D, KV, ST, false, false>(a, tile_ptr(t, page_id(nfull)), lo, ntok - t * kTile, last, lane16, grp);
+        compute_tile<D, KV, QT, ST, false>(last, qop, qop_lo, qmul, t, ntok, grp, st);
       }
     }
 
@@ -696,7 +908,7 @@ void decode_main(const DecodeArgs a) {
       }
     }
     if (steal) {
-      if (threadIdx.x == 0) l_item[0] = stolen;
+      if (threadIdx.x == 0) l_item[0] = first ? request() : stolen;
       __syncthreads();
       next_item = l_item[0];
       __syncthreads();   // l_item and the merge LDS are free for the next item
@@ -704,25 +916,7 @@ void decode_main(const DecodeArgs a) {
       if (shape.P > 1) __syncthreads();   // merge LDS free for reuse
       next_item += gridDim.x;
     }
-  }
-}
-
-// One work-group: decide the split from the device-side lengths, write the
-// item prefix and zero the work counter for decode_main.
-template <int NW>
-__global__ __launch_bounds__(NW * 64) void decode_plan(const DecodeArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  int* red = (int*)smem;            // 2*NW+2 ints (8-byte aligned)
-  int* pre = red + 2 * NW + 2;      // B+1 ints
-  const ItemShape shape = item_shape<NW>(a.U);
-  int tps;
-  const int total = plan_items<NW>(a, pre, red, tps, shape.P, a.UB, a.slots);
-  for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[kPlanHeader + i] = pre[i];
-  if (threadIdx.x == 0) {
-    a.ws_plan[kPlanTps] = tps;
-    a.ws_plan[kPlanTotal] = total;
-    a.ws_plan[kPlanUB] = a.UB;
-    a.ws_plan[kPlanCounter] = 0;
+    first = false;
   }
 }
 

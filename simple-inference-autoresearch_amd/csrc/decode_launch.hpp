@@ -1,6 +1,7 @@
 // Host-side launch of the decode kernels (one instantiation unit per K/V dtype).
 #pragma once
 
+#include <atomic>
 #include <type_traits>
 
 #include "decode_kernel.hpp"
@@ -20,6 +21,14 @@ struct DecodeLaunch {
   hipEvent_t end_event;
 };
 
+// A fresh nonzero id per decode call (tags that call's work counter).
+inline uint32_t next_call_epoch() {
+  static std::atomic<uint32_t> epoch{0};
+  uint32_t e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (e == 0) e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+  return e;
+}
+
 inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
   return (size_t)NW * G16 * D * 4 + (size_t)2 * NW * G16 * 4 + (size_t)(2 * NW + 2) * 4 +
          (size_t)(B + 1) * 4;
@@ -28,19 +37,21 @@ inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
 template <int D, class KV, class QT, class ST>
 int launch_decode_typed(DecodeLaunch& L) {
   constexpr int NW = kDecodeWaves;
-  auto kmain = decode_main<D, KV, QT, ST, NW>;
+  // int8 K/V with fp32 scale rows: one 16-byte scale load per lane when the
+  // rows allow it (decided on the host, compiled as two kernels)
+  auto kmain = decode_main<D, KV, QT, ST, NW, false>;
+  if constexpr (std::is_same<KV, I8>::value && std::is_same<ST, F32>::value)
+    if (L.a.scale_vec) kmain = decode_main<D, KV, QT, ST, NW, true>;
   const size_t lds = decode_lds_bytes(D, L.a.G16, L.a.B, NW);
   const int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
   if (occ <= 0) return fail(SIA_ERR_LAUNCH, "decode kernel does not fit on a CU (LDS %zu B)", lds);
   L.a.slots = device_info().cus * occ;
-  // 1. plan (one work-group), 2. main (persistent, work stealing), 3. split-K merge
-  hipLaunchKernelGGL((decode_plan<NW>), dim3(1), dim3(NW * 64), (size_t)(2 * NW + 2 + L.a.B + 1) * 4, L.stream, L.a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode plan launch: %s", hipGetErrorString(e));
+  L.a.epoch = next_call_epoch();
+  // 1. main (persistent: plans the splits itself, work stealing), 2. split-K merge
   if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
   hipLaunchKernelGGL(kmain, dim3(L.a.slots), dim3(NW * 64), lds, L.stream, L.a);
-  e = hipGetLastError();
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode launch: %s", hipGetErrorString(e));
   if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
