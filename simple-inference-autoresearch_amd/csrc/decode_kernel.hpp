@@ -195,7 +195,7 @@ __device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out,
   // quantum: every wave sharing a unit gets the same number of tiles
   if (!a.kv_per_seq && a.tps_force <= 0) {
     // one length for the whole batch: closed form, item prefix b * per
-    const int n = uniform(seq_tiles(a, 0));
+    const int n = (uniform(seq_tokens(a, 0)) + kTile - 1) / kTile;
     const int tps = plan_uniform(a, n, quantum, UB, slots);
     if (tps > 0) {
       const int per = ceil_div(n, tps, 1.0 / tps) * UB;
@@ -653,6 +653,7 @@ void decode_main(const DecodeArgs a) {
   // decode_reduce and opens this call's work counter.
   int tps;
   const int total = plan_items<NW>(a, pre, red, tps, shape.P, a.UB, (int)gridDim.x);
+  const int tok0 = a.kv_per_seq ? 0 : uniform(seq_tokens(a, 0));
   unsigned long long* counter = (unsigned long long*)(a.ws_plan + kPlanCounter);
   if (blockIdx.x == 0) {
     for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[kPlanHeader + i] = pre[i];
@@ -711,7 +712,8 @@ void decode_main(const DecodeArgs a) {
     const int unit = ublk * shape.units + uin;
     const bool wave_live = uin < shape.units && unit < a.U;
     const int hkv = unit / a.HG, hg = unit - hkv * a.HG;
-    const int ntok = uniform(seq_tokens(a, b));
+    // (a batch-wide length was read once already; per-sequence ones are read here)
+    const int ntok = a.kv_per_seq ? uniform(seq_tokens(a, b)) : tok0;
     const int ntile = (ntok + kTile - 1) / kTile;
     const int nsplit = (ntile + tps - 1) / tps;
     const int t_lo = split * tps;
@@ -920,68 +922,91 @@ void decode_main(const DecodeArgs a) {
   }
 }
 
-// Merge split-K partials of one (sequence, query head) per wave; writes zeros
-// for empty sequences and skips sequences the main kernel wrote directly.
+// Merge split-K partials: each (sequence, query head) row is handled by D/4
+// lanes holding 4 outputs each (16-byte partial loads), so a wave merges
+// 64/(D/4) rows.  Pass 1 takes the max m over the splits (one split per
+// lane of the row's group, repeated per D/4 splits); pass 2 forms the split
+// weights 2^(m_s - M) a group at a time, broadcasts each within the group and
+// accumulates the weighted partials.  Loop bounds are uniform over the wave
+// (the largest split count of its rows), so every shuffle sees all lanes.
+// Rows of sequences the main kernel wrote directly are skipped; empty
+// sequences are written as zeros.
 template <int D, class OT, int NW>
 __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  constexpr int LPR = D / 4;          // lanes per row
+  constexpr int RPW = 64 / LPR;       // rows per wave
   const int lane = threadIdx.x & 63;
-  if (row >= a.B * a.Hq) return;
-  const int b = row / a.Hq, hq = row - b * a.Hq;
-  const int p0 = a.ws_plan[kPlanHeader + b], p1 = a.ws_plan[kPlanHeader + b + 1];
-  const int nsplit = (p1 - p0) / a.UB;
-  if (nsplit == 1) return;
-  const int hkv = hq / a.G, gi = hq - hkv * a.G, hg = gi >> 4, cc = gi & 15;
-  const int unit = hkv * a.HG + hg;
-  const ItemShape shape = item_shape<NW>(a.U);
-  const int ublk = unit / shape.units, uin = unit - ublk * shape.units;
-  char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh;
-  auto slot = [&](int s) { return ((int64_t)(p0 + s * a.UB + ublk) * NW + uin) * a.G16 + cc; };
-  // (m, l) of up to 64 splits per pass, one split per lane
-  float M = -INFINITY;
-  for (int s0 = 0; s0 < nsplit; s0 += 64) {
-    const int s = s0 + lane;
-    const float m = s < nsplit ? a.ws_ml[slot(s) * 2] : -INFINITY;
-    M = fmaxf(M, m);
+  const int li = lane % LPR;
+  const int gbase = lane - li;        // first lane of this row's group
+  const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const bool inr = row < a.B * a.Hq;
+  int nsplit = 1, p0 = 0, b = 0, hq = 0, ublk = 0, uin = 0, cc = 0;
+  if (inr) {
+    b = row / a.Hq;
+    hq = row - b * a.Hq;
+    p0 = a.ws_plan[kPlanHeader + b];
+    nsplit = (a.ws_plan[kPlanHeader + b + 1] - p0) / a.UB;
+    const int hkv = hq / a.G, gi = hq - hkv * a.G;
+    cc = gi & 15;
+    const int unit = hkv * a.HG + (gi >> 4);
+    const ItemShape shape = item_shape<NW>(a.U);
+    ublk = unit / shape.units;
+    uin = unit - ublk * shape.units;
   }
+  const bool work = inr && nsplit != 1;
+  int nmax = work ? nsplit : 0;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-  constexpr int PER = (D + 63) / 64;
-  float A[PER];
+  for (int o = 32; o > 0; o >>= 1) nmax = max(nmax, __shfl_xor(nmax, o));
+  if (!__any(work)) return;   // (wave-uniform) nothing to merge or zero here
+  auto slot = [&](int s) { return ((int64_t)(p0 + s * a.UB + ublk) * NW + uin) * a.G16 + cc; };
+  auto group_max = [&](float x) {
 #pragma unroll
-  for (int i = 0; i < PER; ++i) A[i] = 0.f;
+    for (int o = LPR / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+    return x;
+  };
+  auto group_sum = [&](float x) {
+#pragma unroll
+    for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
+    return x;
+  };
+  float M = -INFINITY;
+  for (int s0 = 0; s0 < nmax; s0 += LPR) {
+    const int s = s0 + li;
+    M = fmaxf(M, (work && s < nsplit) ? a.ws_ml[slot(s) * 2] : -INFINITY);
+  }
+  M = group_max(M);
+  f32x4 A = {0.f, 0.f, 0.f, 0.f};
   float L = 0.f;
-  if (M != -INFINITY) {
-    for (int s0 = 0; s0 < nsplit; s0 += 64) {
-      const int s = s0 + lane;
-      float wt = 0.f, lw = 0.f;
-      if (s < nsplit) {
-        const float m = a.ws_ml[slot(s) * 2];
-        wt = m == -INFINITY ? 0.f : fast_exp2(m - M);
-        lw = wt * a.ws_ml[slot(s) * 2 + 1];
+  for (int s0 = 0; s0 < nmax; s0 += LPR) {
+    const int s = s0 + li;
+    float w = 0.f;
+    if (work && s < nsplit && M != -INFINITY) {
+      const float m = a.ws_ml[slot(s) * 2];
+      w = m == -INFINITY ? 0.f : fast_exp2(m - M);
+      L += w * a.ws_ml[slot(s) * 2 + 1];
+    }
+    // eight partial loads in flight at a time (a row can have tens of splits)
+    const int n = min(LPR, nmax - s0);
+    for (int j0 = 0; j0 < n; j0 += 8) {
+      f32x4 x[8];
+      float wj[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int j = j0 + t;
+        const bool ok = work && j < n && s0 + j < nsplit;
+        x[t] = ok ? *(const f32x4*)(a.ws_acc + slot(s0 + j) * D + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
+        wj[t] = __shfl(w, gbase + (j & (LPR - 1)));
       }
 #pragma unroll
-      for (int o = 32; o > 0; o >>= 1) lw += __shfl_xor(lw, o);
-      L += lw;
-      const int n = min(64, nsplit - s0);
-#pragma unroll 4
-      for (int j = 0; j < n; ++j) {
-        const float w = __shfl(wt, j);
-        const float* src = a.ws_acc + slot(s0 + j) * D;
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-          const int d = lane + 64 * i;
-          if (d < D) A[i] += w * src[d];
-        }
-      }
+      for (int t = 0; t < 8; ++t) A += wj[t] * x[t];
     }
   }
+  L = group_sum(L);
+  if (!work) return;
   const float inv = 1.0f / (L == 0.f ? 1.f : L);
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int d = lane + 64 * i;
-    if (d < D) store_out(OT{}, op + d * (int)sizeof(uint16_t), A[i] * inv);
-  }
+  char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 4 * li * (int)sizeof(uint16_t);
+  *(uint32_t*)op = pack2(OT{}, A[0] * inv, A[1] * inv);
+  *(uint32_t*)(op + 4) = pack2(OT{}, A[2] * inv, A[3] * inv);
 }
 
 }  // namespace sia
