@@ -55,13 +55,37 @@ def run_decode(pkg, case):
                                             case.page_size)
 
 
+SETTLE_MS = 300.0   # set from --settle-ms
+
+
+def settle(fn, ms: float | None = None) -> None:
+    """Run `fn` back to back for about `ms` of wall time before any warm-up.
+
+    An idle MI355X takes tens of milliseconds of sustained load to reach its
+    steady clocks (a prefill kernel measured 193 us over its first launches
+    and 153 us once settled), so short runs would time the ramp rather than
+    the kernel.  This is untimed and separate from the W warm-up steps.
+    """
+    import torch
+
+    budget = (SETTLE_MS if ms is None else ms) / 1e3
+    if budget <= 0:
+        return
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < budget:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_decode(pkg, case, steps: int, warmup: int):
-    """W untimed calls, then exactly `steps` timed calls.
+    """Clock settle, W untimed calls, then exactly `steps` timed calls.
 
     Returns (ms per call for the whole call, list of main-kernel ms per call).
     """
     import torch
 
+    settle(lambda: run_decode(pkg, case))
     for _ in range(warmup):
         run_decode(pkg, case)
     begins = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
@@ -169,6 +193,7 @@ def bench_prefill_config(pkg, steps: int, warmup: int):
     syn = _syn()
     q, k, v = syn.cfg4(torch.device("cuda:0"))
     B, Hq, T, D = q.shape
+    settle(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True))
     for _ in range(warmup):
         pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True)
     e0 = torch.cuda.Event(enable_timing=True)
@@ -228,6 +253,8 @@ def main(argv=None):
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--settle-ms", type=float, default=300.0,
+                   help="untimed back-to-back calls before each config's warm-up, so the GPU clocks settle")
     p.add_argument("--no-others", action="store_true", help="skip configs 2, 4 and 5")
     p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "copy"],
                    help="config to run alone (profiling runs); 'copy' is a plain 1 GiB device copy "
@@ -242,6 +269,8 @@ def main(argv=None):
 
     import torch
 
+    global SETTLE_MS
+    SETTLE_MS = args.settle_ms
     pkg = _pkg()
     pkg.require_library()
     syn = _syn()
@@ -271,6 +300,7 @@ def main(argv=None):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "clock_settle_ms": args.settle_ms,
         "ms_per_step": round(head["us_per_call"] / 1e3, 5),
         "us_per_call": head["us_per_call"],
         "higher_is_better": True,

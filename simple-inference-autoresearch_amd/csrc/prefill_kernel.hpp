@@ -426,20 +426,26 @@ void prefill_fwd(const PrefillArgs a) {
       qk(kstage(PfParity<P + 1>{}), sb0, sb1);
       numer(sa0, sa1, pop);
       pv(vstage(PfParity<P>{}), pop);
+      // the next block's row max (unmasked; redone below on masked blocks)
+      // shares this scheduling region, so its VALU fills the PV MFMA slots
+      rmax = rowmax(sb0, sb1);
       __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // 4 K operand reads ahead
 #pragma unroll
       for (int i = 0; i < 2 * KST; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one S MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // next operand read
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);   // softmax VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // softmax VALU
       }
 #pragma unroll
       for (int i = 0; i < 4 * ET; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one PV MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // softmax / row-max VALU
       }
-      if (j + 1 >= wfull) mask(sb0, sb1, (j + 1) * kPfBN);
-      rmax = rowmax(sb0, sb1);
+      if (j + 1 >= wfull) {
+        mask(sb0, sb1, (j + 1) * kPfBN);
+        rmax = rowmax(sb0, sb1);
+      }
     }
   };
 
