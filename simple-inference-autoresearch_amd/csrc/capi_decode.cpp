@@ -24,12 +24,12 @@ size_t plan_bytes(int B) { return (size_t)round_up((int64_t)(kPlanHeader + B + 1
 // One item holds a partial for each of its kDecodeWaves unit slots.
 size_t item_bytes(const Geometry& g) { return (size_t)kDecodeWaves * g.G16 * (g.D + 2) * 4; }
 
-// Items the workspace must be able to hold: the split planner keeps the item
-// count near a few per persistent work-group (at most 4 groups per CU), plus
-// one per (sequence, unit block) (see plan_items in decode_kernel.hpp).
+// Partial slots the workspace must hold: two per persistent work-group (its
+// first and last segment may each be a piece of a split sequence), for up to
+// four groups per CU, plus slack.
 int64_t wanted_items(const Geometry& g) {
   const int cus = device_info().cus > 0 ? device_info().cus : 256;
-  return 8LL * cus * 4 + (int64_t)g.B * g.UB + 64;
+  return 2LL * cus * 4 + 64;
 }
 
 int geometry(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, Geometry& g) {
@@ -195,11 +195,13 @@ int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decod
     L.begin_event = (hipEvent_t)opts->main_begin_event;
     L.end_event = (hipEvent_t)opts->main_end_event;
   }
+  // the work line (B x tiles x unit blocks) is indexed with 32-bit integers
+  if ((int64_t)g.B * ((L.a.cap_tokens + kTile - 1) / kTile) * g.UB > 0x7fffffffLL)
+    return fail(SIA_ERR_UNSUPPORTED, "batch x cache capacity too large (more than 2^31 tiles of work)");
   const size_t pb = plan_bytes(g.B);
   const size_t ib = item_bytes(g);
-  if (ws == nullptr || bytes < pb + ib * (size_t)g.B * g.UB || !aligned16(ws))
-    return fail(SIA_ERR_WORKSPACE, "decode workspace missing, misaligned or smaller than %zu bytes",
-                pb + ib * (size_t)g.B * g.UB);
+  if (ws == nullptr || bytes < pb + ib * 2 || !aligned16(ws))
+    return fail(SIA_ERR_WORKSPACE, "decode workspace missing, misaligned or smaller than %zu bytes", pb + ib * 2);
   int64_t items = (int64_t)((bytes - pb) / ib);
   if (items > 0x7fffffff) items = 0x7fffffff;
   DecodeArgs& a = L.a;

@@ -10,18 +10,20 @@
 // serving its whole query-head group).
 //
 // Work decomposition (MI355X-first, not the reference's):
-//  * A work item is (sequence b, split s, unit u) where a unit is one KV head
-//    and a group of up to 16 of its query heads.  Each item covers
-//    `tps` 16-token tiles of the sequence; `tps` is chosen on the device from
-//    kv_len so that the persistent grid (CUs x occupancy work-groups) gets an
-//    even share (plan_items below).  The KV of a unit is read once for all of
-//    its query heads.
-//  * A work-group of NW wave64s takes items round-robin.  Its waves split the
+//  * A unit is one KV head and a group of up to 16 of its query heads; the
+//    KV of a unit is read once for all of its query heads.  The work of a
+//    call is a line of 16-token tiles (sequence-major, then block of units,
+//    then tile) whose length W comes from kv_len on the device.  The
+//    persistent grid (CUs x occupancy work-groups) splits it stream-K style:
+//    each group takes an equal contiguous share, cut into segments at
+//    (sequence, unit block) boundaries, so ragged batches stay balanced with
+//    no work queue.
+//  * Within a segment the group's NW wave64s cover NW units.  Its waves split the
 //    item's 16-token tiles (double-buffered in registers); each wave runs its
 //    own online softmax and the waves' (m, l, acc) states are merged through
-//    LDS.  A sequence that fits one item is normalised and written straight to
-//    `out`; otherwise the item writes an fp32 partial and decode_reduce()
-//    merges the splits.
+//    LDS.  A segment that covers its whole (sequence, unit block) is
+//    normalised and written straight to `out`; otherwise it writes an fp32
+//    partial and decode_reduce() merges the pieces.
 //  * Per tile a wave computes S^T = K Q^T with v_mfma_f32_16x16x32 (tokens as
 //    rows, query heads as columns) and O^T += V^T P^T with v_mfma_f32_16x16x16
 //    (head_dim as rows), whose B operand layout is exactly the S^T output
@@ -39,12 +41,12 @@
 namespace sia {
 
 constexpr int kTile = 16;          // tokens per MFMA tile
-// Plan header in the workspace (ints): split size, item count, unit blocks per
-// (sequence, split), a pad, the 64-bit work counter (ints 4-5: call epoch in
-// the high half, items handed out in the low half); the item prefix per
-// sequence follows.
-constexpr int kPlanTps = 0, kPlanTotal = 1, kPlanUB = 2, kPlanCounter = 4, kPlanHeader = 6;
-constexpr int kTpsMin = 8;         // smallest split, in tiles
+// Plan header in the workspace (ints), written by work-group 0 of decode_main
+// for decode_reduce: total work W (tiles x unit blocks), the number G of
+// work-groups that share it, the unit blocks per sequence; the work prefix
+// per sequence (B+1 ints) follows.
+constexpr int kPlanW = 0, kPlanG = 1, kPlanUB = 2, kPlanHeader = 4;
+constexpr int kMinGroupTiles = 8;  // least work per work-group, in tiles
 // The running max is only raised when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^8: well inside f16/bf16 range, and the
 // rescale of (l, acc) almost never runs after the first tile.
@@ -68,7 +70,6 @@ struct DecodeArgs {
   int32_t tps_force;
   int32_t slots;                                     // persistent work-groups of decode_main
   int32_t scale_vec;                                 // scale rows allow 16-byte vector loads
-  uint32_t epoch;                                    // nonzero id of this call (tags the work counter)
   // 32-bit copies of the per-tile strides (bytes): page strides (0 when
   // contiguous) and token strides, so the tile address needs only 32x32->64
   // products
@@ -164,117 +165,31 @@ __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pr
 // candidate wins (ties go to the larger split, i.e. fewer partials).  With
 // equal lengths this finds the exact balance; with ragged lengths it keeps
 // the heaviest slot close to the mean.
-constexpr int kItemOverhead = 8;   // per-item fixed cost of the split planner, in tiles
-
-// The planner's choice when every sequence has the same length (n tiles):
-// lane c of each wave scores c+1 splits and the wave takes the arg-min, so
-// each wave reaches the same answer with no block-wide step.  Returns 0 when
-// no candidate fits the partial workspace.
-__device__ __forceinline__ int plan_uniform(const DecodeArgs& a, int n, int quantum, int UB, int slots) {
-  const int c = (threadIdx.x & 63) + 1;
-  int t = ceil_div(n, c, 1.0 / c);
-  t = max(t, kTpsMin);
-  t = (t + quantum - 1) / quantum * quantum;
-  const long long items = (long long)a.B * ceil_div(n, t, 1.0 / t) * UB;
-  constexpr long long kInf = (1LL << 36) - 1;
-  long long cost = kInf;
-  if (items <= a.max_items) cost = min(kInf, (long long)ceil_div((int)items, slots, 1.0 / slots) * (t + kItemOverhead));
-  unsigned long long k = ((unsigned long long)cost << 27) | (unsigned long long)(0x7ffffff - t);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long y = __shfl_xor(k, o);
-    k = y < k ? y : k;
+// The work line of one call: sequence-major, then unit block, then 16-token
+// tile; pre[b] = position of sequence b's first tile (pre[B] = W).  One
+// length for the whole batch has a closed form; per-sequence lengths take a
+// block-wide scan.
+template <int NW>
+__device__ int plan_work(const DecodeArgs& a, int* pre, int* red, int tok0) {
+  const int T = NW * 64;
+  if (!a.kv_per_seq) {
+    const int per = ((tok0 + kTile - 1) / kTile) * a.UB;
+    for (int b = threadIdx.x; b <= a.B; b += T) pre[b] = b * per;
+    __syncthreads();
+    return a.B * per;
   }
-  if ((long long)(k >> 27) >= kInf) return 0;
-  return uniform(0x7ffffff - (int)(k & 0x7ffffffULL));
+  for (int b = threadIdx.x; b < a.B; b += T) pre[b] = seq_tiles(a, b);
+  __syncthreads();
+  block_scan<NW>(a, 1, pre, red, a.UB);
+  return pre[a.B];
 }
 
-template <int NW>
-__device__ int plan_items(const DecodeArgs& a, int* pre, int* red, int& tps_out, int quantum, int UB, int slots) {
-  const int T = NW * 64;
-  // quantum: every wave sharing a unit gets the same number of tiles
-  if (!a.kv_per_seq && a.tps_force <= 0) {
-    // one length for the whole batch: closed form, item prefix b * per
-    const int n = (uniform(seq_tokens(a, 0)) + kTile - 1) / kTile;
-    const int tps = plan_uniform(a, n, quantum, UB, slots);
-    if (tps > 0) {
-      const int per = ceil_div(n, tps, 1.0 / tps) * UB;
-      for (int b = threadIdx.x; b <= a.B; b += T) pre[b] = b * per;
-      __syncthreads();
-      tps_out = tps;
-      return a.B * per;
-    }
-  }
-  // lengths (in tiles) into pre[] temporarily, and the longest
-  int mx = 0;
-  for (int b = threadIdx.x; b < a.B; b += T) {
-    const int t = seq_tiles(a, b);
-    pre[b] = t;
-    mx = max(mx, t);
-  }
-  long long dummy = 0;
-  block_sum_max<NW>(dummy, mx, red);
-  int tps;
-  bool fits = false;   // the chosen split is known to fit the partial workspace
-  if (a.tps_force > 0) {
-    tps = a.tps_force;
-  } else {
-    // candidate c = threadIdx.x / 8 + 1 splits of the longest sequence; the 8
-    // threads of a candidate sum the item counts of every 8th sequence
-    static_assert(NW * 64 >= 8, "need at least 8 threads");
-    const int c = threadIdx.x / 8 + 1, j = threadIdx.x & 7;
-    int t = ceil_div(mx, c, 1.0 / c);
-    t = max(t, kTpsMin);
-    t = (t + quantum - 1) / quantum * quantum;
-    const double rt = 1.0 / t;
-    // item counts saturate just above the workspace capacity (such a split is out)
-    const int sat = min(a.max_items / UB, 0x7ffffffe) + 1;
-    auto sadd = [sat](int x, int y) { return y >= sat - x ? sat : x + y; };   // x, y in [0, sat]
-    int items = 0;
-    for (int b = j; b < a.B; b += 8) items = sadd(items, ceil_div(pre[b], t, rt));
-    items = sadd(items, __shfl_xor(items, 1));
-    items = sadd(items, __shfl_xor(items, 2));
-    items = sadd(items, __shfl_xor(items, 4));
-    constexpr long long kInf = (1LL << 36) - 1;
-    long long cost = kInf;
-    if (items < sat) {
-      const long long all = (long long)items * UB;
-      cost = (long long)ceil_div((int)min(all, (long long)0x7fffffff), slots, 1.0 / slots) * (t + kItemOverhead);
-      if (all > a.max_items || cost > kInf) cost = kInf;
-    }
-    // arg-min over the block of (cost, -t): ties prefer the larger split
-    unsigned long long k = ((unsigned long long)cost << 27) | (unsigned long long)(0x7ffffff - t);
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const unsigned long long y = __shfl_xor(k, o);
-      k = y < k ? y : k;
-    }
-    __syncthreads();
-    unsigned long long* red64 = (unsigned long long*)red;   // NW 8-byte slots (red is 8-byte aligned)
-    if ((threadIdx.x & 63) == 0) red64[threadIdx.x >> 6] = k;
-    __syncthreads();
-    unsigned long long best = red64[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) best = red64[w] < best ? red64[w] : best;
-    tps = 0x7ffffff - (int)(best & 0x7ffffffULL);
-    fits = (long long)(best >> 27) < kInf;
-  }
-  tps = max(tps, kTpsMin);
-  tps = (tps + quantum - 1) / quantum * quantum;
-  // Grow the split until the partial workspace can hold every item.
-  for (int guard = 0; guard < 32 && !fits; ++guard) {
-    long long items = 0;
-    const double rt = 1.0 / tps;
-    for (int b = threadIdx.x; b < a.B; b += T) items += (long long)ceil_div(pre[b], tps, rt) * UB;
-    int dm = 0;
-    block_sum_max<NW>(items, dm, red);
-    if (items <= a.max_items) break;
-    tps = min(tps * 2, 1 << 28);
-  }
-  __syncthreads();
-  block_scan<NW>(a, tps, pre, red, UB);
-  tps_out = tps;
-  return pre[a.B];
+// Stream-K split of W tiles over G work-groups: group g takes
+// [lo(g), lo(g+1)) with lo(g) = floor(g W / G); the group holding position x
+// is ceil((x+1) G / W) - 1.
+__device__ __forceinline__ int sk_lo(int g, int W, int G) { return (int)((int64_t)g * W / G); }
+__device__ __forceinline__ int sk_group(int x, int W, int G) {
+  return (int)(((int64_t)(x + 1) * G + W - 1) / W) - 1;
 }
 
 // -------------------------------------------------------------- tile data
@@ -648,41 +563,28 @@ void decode_main(const DecodeArgs a) {
   int* pre = red + 2 * NW + 2;
 
   const ItemShape shape = item_shape<NW>(a.U);
-  // The split plan, computed by every work-group from the device-side
-  // lengths (the same in every group).  Group 0 publishes it for
-  // decode_reduce and opens this call's work counter.
-  int tps;
-  const int total = plan_items<NW>(a, pre, red, tps, shape.P, a.UB, (int)gridDim.x);
+  // The work line (every work-group computes the same prefix) and its
+  // stream-K split: group g takes an equal contiguous share, so groups finish
+  // together whatever the lengths, with no queue or atomics.  Group 0 records
+  // the split for decode_reduce.
   const int tok0 = a.kv_per_seq ? 0 : uniform(seq_tokens(a, 0));
-  unsigned long long* counter = (unsigned long long*)(a.ws_plan + kPlanCounter);
+  const int W = plan_work<NW>(a, pre, red, tok0);
+  int G = (int)gridDim.x;
+  if (a.tps_force > 0) G = min(G, max(1, (W + a.tps_force - 1) / a.tps_force));   // forced share (tests)
+  G = min(G, max(1, (W + kMinGroupTiles - 1) / kMinGroupTiles));
+  G = min(G, max(1, a.max_items / 2));                      // two partial slots per group
   if (blockIdx.x == 0) {
     for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[kPlanHeader + i] = pre[i];
     if (threadIdx.x == 0) {
-      a.ws_plan[kPlanTps] = tps;
-      a.ws_plan[kPlanTotal] = total;
+      a.ws_plan[kPlanW] = W;
+      a.ws_plan[kPlanG] = G;
       a.ws_plan[kPlanUB] = a.UB;
-      atomicExch(counter, (unsigned long long)a.epoch << 32);
     }
   }
-  // Work assignment: group g first takes item g; items past the grid are
-  // handed out by the counter, so a group that finishes early takes more and
-  // ragged batches stay balanced.  A group asks for its second item only when
-  // its first is done (long after group 0 opened the counter), and for each
-  // later one as that item starts.  A count carrying another call's epoch
-  // (the counter not opened yet) reads as "no item": the group stops, and the
-  // groups still running, group 0 among them, take what is left.  An item
-  // handed out twice is computed twice with identical results.
-  int* l_item = red;   // LDS slot broadcasting the next item
+  const int g = blockIdx.x;
+  const int x_hi = g < G ? sk_lo(g + 1, W, G) : 0;
+  int x = g < G ? sk_lo(g, W, G) : 0;
   int* prog = red + 2;   // tiles done per wave (NW ints; read and written without barriers)
-  const uint32_t steal_range = total > (int)gridDim.x ? (uint32_t)(total - (int)gridDim.x) : 0u;
-  const bool steal = steal_range > 0;
-  auto request = [&]() -> int {
-    const unsigned long long old = atomicAdd(counter, 1ull);
-    const uint32_t n = (uint32_t)old;
-    return ((uint32_t)(old >> 32) == a.epoch && n < steal_range) ? (int)gridDim.x + (int)n : total;
-  };
-  bool first = true;
-  int next_item = blockIdx.x;
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -697,27 +599,29 @@ void decode_main(const DecodeArgs a) {
   const int uin = wave / shape.P;        // unit slot of this wave inside an item
   const int phase = wave - uin * shape.P;
 
-  while (next_item < total) {
-    const int item = uniform(next_item);
-    // request the following item now (after the first); its index is only
-    // needed at the end
-    int stolen = total;
-    if (steal && !first && threadIdx.x == 0) stolen = request();
-    // item -> (b, split, unit block): b is the largest index with pre[b] <= item
+  // Segments: the maximal pieces of [x, x_hi) inside one (sequence, unit
+  // block).  A segment that covers its whole (b, ublk) is written straight to
+  // `out`; a piece writes a partial to slot 2g (the group's first segment) or
+  // 2g+1 (its last), which decode_reduce finds from the same split.
+  bool first_seg = true;
+  while (x < x_hi) {
+    // b: the largest index with pre[b] <= x
     int blo = 0, bhi = a.B;
-    while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= item) blo = mid; else bhi = mid; }
+    while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= x) blo = mid; else bhi = mid; }
     const int b = uniform(blo);
-    const int rem = uniform(item - pre[b]);
-    const int split = rem / a.UB, ublk = rem - split * a.UB;
-    const int unit = ublk * shape.units + uin;
-    const bool wave_live = uin < shape.units && unit < a.U;
-    const int hkv = unit / a.HG, hg = unit - hkv * a.HG;
     // (a batch-wide length was read once already; per-sequence ones are read here)
     const int ntok = a.kv_per_seq ? uniform(seq_tokens(a, b)) : tok0;
     const int ntile = (ntok + kTile - 1) / kTile;
-    const int nsplit = (ntile + tps - 1) / tps;
-    const int t_lo = split * tps;
-    const int t_hi = min(t_lo + tps, ntile);
+    const int rem = uniform(x - pre[b]);
+    const int ublk = rem / ntile;
+    const int t_lo = rem - ublk * ntile;
+    const int seg_end = min(x_hi, pre[b] + (ublk + 1) * ntile);
+    const int t_hi = t_lo + (seg_end - x);
+    const bool direct = t_lo == 0 && t_hi == ntile;
+    const int pslot_id = first_seg ? 2 * g : 2 * g + 1;
+    const int unit = ublk * shape.units + uin;
+    const bool wave_live = uin < shape.units && unit < a.U;
+    const int hkv = unit / a.HG, hg = unit - hkv * a.HG;
     const int nh = wave_live ? min(16, a.G - 16 * hg) : 0;    // live head columns of this wave's unit
     const bool live = lane16 < nh;
     const int hq = live ? hkv * a.G + 16 * hg + lane16 : 0;
@@ -834,9 +738,8 @@ void decode_main(const DecodeArgs a) {
 
     const float lsum = wave_sum_xor16_32(st.l);
     const float unscale = std::is_same<KV, I8>::value ? ldexpf(1.0f, st.sexp - 4) : 1.0f;
-    const bool direct = nsplit == 1;
-    // partial slot of (item, unit slot, head col)
-    const int64_t pslot = ((int64_t)item * NW + uin) * a.G16;
+    // partial slot of (segment, unit slot, head col)
+    const int64_t pslot = ((int64_t)pslot_id * NW + uin) * a.G16;
     if (shape.P == 1) {
       // one wave owns each unit: write straight from registers
       if (live) {
@@ -903,22 +806,15 @@ void decode_main(const DecodeArgs a) {
           char* op = a.out + b * a.o_sb + (int64_t)hqo * a.o_sh + d * (int)sizeof(uint16_t);
           store_out(QT{}, op, A / (L == 0.f ? 1.f : L));
         } else {
-          const int64_t ps = ((int64_t)item * NW + us) * a.G16 + cc;
+          const int64_t ps = ((int64_t)pslot_id * NW + us) * a.G16 + cc;
           a.ws_acc[ps * D + d] = A;
           if (d == 0) { a.ws_ml[ps * 2 + 0] = M; a.ws_ml[ps * 2 + 1] = L; }
         }
       }
     }
-    if (steal) {
-      if (threadIdx.x == 0) l_item[0] = first ? request() : stolen;
-      __syncthreads();
-      next_item = l_item[0];
-      __syncthreads();   // l_item and the merge LDS are free for the next item
-    } else {
-      if (shape.P > 1) __syncthreads();   // merge LDS free for reuse
-      next_item += gridDim.x;
-    }
-    first = false;
+    if (shape.P > 1) __syncthreads();   // merge LDS free for reuse
+    x = seg_end;
+    first_seg = false;
   }
 }
 
@@ -940,25 +836,40 @@ __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
   const int gbase = lane - li;        // first lane of this row's group
   const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
   const bool inr = row < a.B * a.Hq;
-  int nsplit = 1, p0 = 0, b = 0, hq = 0, ublk = 0, uin = 0, cc = 0;
+  const int W = a.ws_plan[kPlanW], G = a.ws_plan[kPlanG];
+  // pieces of this row's (sequence, unit block): one per work-group in
+  // [gf, gf + nsplit); the first group's piece is its first segment (slot
+  // 2g) only if the range starts exactly at the group's start
+  int nsplit = 1, gf = 0, s_first = 0, b = 0, hq = 0, uin = 0, cc = 0;
   if (inr) {
     b = row / a.Hq;
     hq = row - b * a.Hq;
-    p0 = a.ws_plan[kPlanHeader + b];
-    nsplit = (a.ws_plan[kPlanHeader + b + 1] - p0) / a.UB;
+    const int pb = a.ws_plan[kPlanHeader + b];
+    const int ntile = (a.ws_plan[kPlanHeader + b + 1] - pb) / a.UB;
     const int hkv = hq / a.G, gi = hq - hkv * a.G;
     cc = gi & 15;
     const int unit = hkv * a.HG + (gi >> 4);
     const ItemShape shape = item_shape<NW>(a.U);
-    ublk = unit / shape.units;
+    const int ublk = unit / shape.units;
     uin = unit - ublk * shape.units;
+    if (ntile == 0) {
+      nsplit = 0;                                   // empty sequence: zeros
+    } else {
+      const int x0 = pb + ublk * ntile;
+      gf = sk_group(x0, W, G);
+      nsplit = sk_group(x0 + ntile - 1, W, G) - gf + 1;
+      s_first = x0 != sk_lo(gf, W, G) ? 1 : 0;
+    }
   }
   const bool work = inr && nsplit != 1;
   int nmax = work ? nsplit : 0;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) nmax = max(nmax, __shfl_xor(nmax, o));
   if (!__any(work)) return;   // (wave-uniform) nothing to merge or zero here
-  auto slot = [&](int s) { return ((int64_t)(p0 + s * a.UB + ublk) * NW + uin) * a.G16 + cc; };
+  auto slot = [&](int s) {
+    const int id = 2 * (gf + s) + (s == 0 ? s_first : 0);
+    return ((int64_t)id * NW + uin) * a.G16 + cc;
+  };
   auto group_max = [&](float x) {
 #pragma unroll
     for (int o = LPR / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));

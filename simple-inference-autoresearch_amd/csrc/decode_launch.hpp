@@ -1,7 +1,6 @@
 // Host-side launch of the decode kernels (one instantiation unit per K/V dtype).
 #pragma once
 
-#include <atomic>
 #include <type_traits>
 
 #include "decode_kernel.hpp"
@@ -21,14 +20,6 @@ struct DecodeLaunch {
   hipEvent_t end_event;
 };
 
-// A fresh nonzero id per decode call (tags that call's work counter).
-inline uint32_t next_call_epoch() {
-  static std::atomic<uint32_t> epoch{0};
-  uint32_t e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
-  if (e == 0) e = epoch.fetch_add(1, std::memory_order_relaxed) + 1;
-  return e;
-}
-
 inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
   return (size_t)NW * G16 * D * 4 + (size_t)2 * NW * G16 * 4 + (size_t)(2 * NW + 2) * 4 +
          (size_t)(B + 1) * 4;
@@ -46,8 +37,7 @@ int launch_decode_typed(DecodeLaunch& L) {
   const int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
   if (occ <= 0) return fail(SIA_ERR_LAUNCH, "decode kernel does not fit on a CU (LDS %zu B)", lds);
   L.a.slots = device_info().cus * occ;
-  L.a.epoch = next_call_epoch();
-  // 1. main (persistent: plans the splits itself, work stealing), 2. split-K merge
+  // 1. main (persistent, stream-K share per group), 2. merge of the split pieces
   if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
   hipLaunchKernelGGL(kmain, dim3(L.a.slots), dim3(NW * 64), lds, L.stream, L.a);
