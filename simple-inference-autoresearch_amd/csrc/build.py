@@ -42,16 +42,11 @@ def sources():
 
 
 # Extra flags per source: the decode kernels keep their MFMA accumulators in
-# VGPRs (no AGPR round trips around the online-softmax rescale), and their one
-# work-stealing atomic (issued by a single lane, reply needed only when the
-# item ends) is left alone by the atomic optimizer, whose wave-wide rewrite
-# would wait for the reply at once.
-_NO_ATOMIC_OPT = ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
+# VGPRs (no AGPR round trips around the online-softmax rescale).
 EXTRA_FLAGS = {
-    "decode_f16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", *_NO_ATOMIC_OPT],
-    "decode_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", *_NO_ATOMIC_OPT],
-    "decode_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", *_NO_ATOMIC_OPT],
-    "decode_d256.hip": _NO_ATOMIC_OPT,
+    "decode_f16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "decode_bf16.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "decode_i8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 
