@@ -360,17 +360,22 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
 
   float s[4];
   if constexpr (kInt8) {
-    // int8 K against the int8 query halves (q = step * (hi + lo/254)):
-    // exact integer dot products, no conversion of K
-    i32x4 shi = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
+    // int8 K against the three int8 query terms (q = step * (hi + mid/254 +
+    // lo/254^2), hi and mid in qop, lo in qop_lo): exact integer dot
+    // products, no conversion of K
+    i32x4 shi = {0, 0, 0, 0}, smid = {0, 0, 0, 0}, slo = {0, 0, 0, 0};
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) {
       const u32x4 ka = {c.k.w[4 * j], c.k.w[4 * j + 1], c.k.w[4 * j + 2], c.k.w[4 * j + 3]};
       shi = mfma16x16x64_i8(ka, qop[j], shi);
+      smid = mfma16x16x64_i8(ka, qop[D / 64 + j], smid);
       slo = mfma16x16x64_i8(ka, qop_lo[j], slo);
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = (float)(__mul24(shi[i], 254) + slo[i]) * (qmul * c.ks[i]);
+    for (int i = 0; i < 4; ++i) {
+      const int t = __mul24(shi[i], 254) + smid[i];          // |t| < 2^30: exact
+      s[i] = __builtin_fmaf((float)t, 254.0f, (float)slo[i]) * (qmul * c.ks[i]);
+    }
   } else {
     f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -470,34 +475,41 @@ __device__ __forceinline__ float prep_q(const DecodeArgs& a, const QRaw<D>& raw,
   }
   float mul = a.qk_scale;
   if constexpr (std::is_same<KV, I8>::value) {
-    // int8 K: the query becomes two int8 vectors, q = step * (hi + lo/254)
-    // with step = max|q| / 127, |hi|, |lo| <= 127 (error <= step/508 per
-    // element).  Byte order follows the lane's elements, as K's bytes do.
+    // int8 K: the query becomes three int8 vectors, q = step * (hi + mid/254
+    // + lo/254^2) with step = max|q| / 127 and |hi|, |mid|, |lo| <= 127
+    // (error <= step/129032 per element, finer than an f16 query for every
+    // element within 2^9 of the max: a few outlier channels cost nothing).
+    // Byte order follows the lane's elements, as K's bytes do.  hi and mid
+    // go to qop[0, D/64) and qop[D/64, D/32), lo to qop_lo[0, D/64).
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) amax = fmaxf(amax, fabsf(qf[i]));
     amax = wave_max_xor16_32(amax);
     const float inv = amax > 0.f ? 127.0f / amax : 0.f;
-    uint32_t hw[PER / 4], lw[PER / 4];
+    uint32_t hw[PER / 4], mw[PER / 4], lw[PER / 4];
 #pragma unroll
     for (int w = 0; w < PER / 4; ++w) {
-      uint32_t h4 = 0, l4 = 0;
+      uint32_t h4 = 0, m4 = 0, l4 = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float y = qf[4 * w + i] * inv;
         const float h = rintf(y);
-        const int lo = (int)rintf((y - h) * 254.0f);
+        const float r = (y - h) * 254.0f;
+        const float m = rintf(r);
+        const int lo = (int)rintf((r - m) * 254.0f);
         h4 |= ((uint32_t)(int)h & 0xffu) << (8 * i);
+        m4 |= ((uint32_t)(int)m & 0xffu) << (8 * i);
         l4 |= ((uint32_t)lo & 0xffu) << (8 * i);
       }
-      hw[w] = h4; lw[w] = l4;
+      hw[w] = h4; mw[w] = m4; lw[w] = l4;
     }
 #pragma unroll
     for (int j = 0; j < D / 64; ++j) {
       qop[j] = u32x4{hw[4 * j], hw[4 * j + 1], hw[4 * j + 2], hw[4 * j + 3]};
+      qop[D / 64 + j] = u32x4{mw[4 * j], mw[4 * j + 1], mw[4 * j + 2], mw[4 * j + 3]};
       qop_lo[j] = u32x4{lw[4 * j], lw[4 * j + 1], lw[4 * j + 2], lw[4 * j + 3]};
     }
-    return amax > 0.f ? mul * (amax / (127.0f * 254.0f)) : 0.f;
+    return amax > 0.f ? mul * (amax / (127.0f * 254.0f * 254.0f)) : 0.f;
   }
   if constexpr (std::is_same<MT, F16>::value) {
     // Scale the query by a power of two so that max|q| lies in [2^13, 2^14):

@@ -191,6 +191,42 @@ def test_paged_small_head_dims(gpu_pkg, kv, D):
     assert torch.all(out[1] == 0)
 
 
+@pytest.mark.parametrize("ratio", [1.0, 100.0, 1000.0])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_int8_query_outlier_channels(gpu_pkg, ratio, D):
+    """int8 K runs QK on the int8 MFMA with the query split into two int8
+    vectors scaled by max|q|: queries whose few outlier channels are `ratio`
+    times the rest must still meet the int8 bar (1e-2 vs the dequantised
+    oracle)."""
+    announce(f"int8 query outliers ratio={ratio} D={D}")
+    case = _syn().paged_case([700, 1500, 33, 4096], Hq=32, Hkv=8, D=D, page=16, seed=21, device=DEV,
+                             kv="int8")
+    q = case.q.float()
+    g = torch.Generator(device=DEV).manual_seed(5)
+    chans = torch.randperm(D, generator=g, device=DEV)[:3]
+    q[..., chans] *= ratio
+    case.q = q.to(case.q.dtype)
+    out = run_paged(gpu_pkg, case)
+    torch.cuda.synchronize()
+    err = assert_close(out, oracle_paged(case), 1e-2, f"outliers x{ratio} D={D}")
+    print(f"max err {err:.2e}")
+
+
+def test_many_short_sequences(gpu_pkg):
+    """A large ragged batch of short (and empty) sequences: each work-group's
+    share of the work line spans many sequences, most written directly."""
+    announce("600 short sequences")
+    rng = np.random.default_rng(7)
+    ctx = [int(x) for x in rng.integers(0, 81, size=600)]
+    ctx[::37] = [0] * len(ctx[::37])
+    case = _syn().paged_case(ctx, Hq=32, Hkv=8, D=128, page=16, seed=22, device=DEV, kv="int8")
+    out = run_paged(gpu_pkg, case)
+    torch.cuda.synchronize()
+    assert_close(out, oracle_paged(case), 2e-3, "600 short sequences")
+    for b in range(0, 600, 37):
+        assert torch.all(out[b] == 0)
+
+
 @pytest.mark.parametrize("tps", [0, 8, 12, 16, 40, 64])
 def test_split_count_invariance(gpu_pkg, tps):
     """Any split of the sequence merges to the same result (and the oracle's)."""
