@@ -211,6 +211,46 @@ def bench_prefill_config(pkg, steps: int, warmup: int):
             "algorithmic_flops": flops, "workload": "config 4: causal prefill bf16 B4 T2048 32/8 heads D128"}
 
 
+def rope_bytes(B: int, T: int, Hq: int, Hkv: int, D: int, es: int = 2) -> int:
+    """Algorithmic bytes of one fused RoPE call: read q, k and one cos and one sin row per
+    token, write q_rot, k_rot (the reference's convention,
+    benchmarks/benchmark_kernel/bench_rope_compare.py:28-34)."""
+    return (2 * B * T * (Hq + Hkv) * D + 2 * T * D) * es
+
+
+def bench_rope_config(pkg, steps: int, warmup: int):
+    """Fused q/k RoPE (bf16, Llama-3-8B heads 32/8, D128, Llama 3 tables): a long prefill
+    (B1 T8192, HBM-bound) and a decode step (B64 T1, one table row)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    rf = pkg.RopeFrequencies(128, 8192, device=dev)
+    out = {}
+    for label, B, T in (("prefill_B1_T8192", 1, 8192), ("decode_B64_T1", 64, 1)):
+        g = torch.Generator(device=dev).manual_seed(7)
+        q = torch.randn(B, T, 32, 128, device=dev, dtype=torch.bfloat16, generator=g)
+        k = torch.randn(B, T, 8, 128, device=dev, dtype=torch.bfloat16, generator=g)
+        cos, sin = rf.get(T, start_pos=0 if T > 1 else 4000, dtype=torch.bfloat16)
+        settle(lambda: pkg.rope_triton(q, k, cos, sin))
+        for _ in range(warmup):
+            pkg.rope_triton(q, k, cos, sin)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            pkg.rope_triton(q, k, cos, sin)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        nbytes = rope_bytes(B, T, 32, 8, 128)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[label] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                      "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+    out["workload"] = "fused q/k RoPE bf16, 32/8 heads D128, split-half, Llama 3 tables"
+    return out
+
+
 def bench_copy(steps: int, warmup: int, nbytes: int = 1 << 30):
     """A plain device-to-device copy of `nbytes` (torch's copy kernel).
 
@@ -255,8 +295,8 @@ def main(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--settle-ms", type=float, default=300.0,
                    help="untimed back-to-back calls before each config's warm-up, so the GPU clocks settle")
-    p.add_argument("--no-others", action="store_true", help="skip configs 2, 4 and 5")
-    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "copy"],
+    p.add_argument("--no-others", action="store_true", help="skip configs 2, 4, 5 and the RoPE lines")
+    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "rope", "copy"],
                    help="config to run alone (profiling runs); 'copy' is a plain 1 GiB device copy "
                         "that calibrates the HBM byte counters")
     args = p.parse_args(argv)
@@ -280,6 +320,10 @@ def main(argv=None):
     if args.config == "copy":   # counter calibration: 1 GiB read + 1 GiB written per launch
         r = bench_copy(args.steps, args.warmup)
         print(json.dumps({"config": "copy", **r}), flush=True)
+        return 0
+    if args.config == "rope":   # fused RoPE only (profiling runs)
+        r = bench_rope_config(pkg, args.steps, args.warmup)
+        print(json.dumps({"config": "rope", **r}), flush=True)
         return 0
     if args.config == "cfg4":   # prefill only (profiling runs)
         r = bench_prefill_config(pkg, args.steps, args.warmup)
@@ -345,6 +389,8 @@ def main(argv=None):
             torch.cuda.empty_cache()
         others["cfg4"] = bench_prefill_config(pkg, max(20, args.steps // 2), args.warmup)
         print(f"[bench] cfg4: {others['cfg4']}", file=sys.stderr, flush=True)
+        others["rope"] = bench_rope_config(pkg, max(20, args.steps // 2), args.warmup)
+        print(f"[bench] rope: {others['rope']}", file=sys.stderr, flush=True)
         result["other_configs"] = others
         case = None
 

@@ -188,6 +188,22 @@ int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_d
                  const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst, const sia_tensor* block_table,
                  const sia_tensor* start_pos, int32_t start_pos_host, int32_t page_size, void* stream);
 
+/* Rotary position embedding of Q and K in one launch.  Replaces the Triton
+ * kernel _rope_qk_fwd and its wrapper (kernels/rope_kernel.py:86-165,
+ * 193-285), which ops/rope.py:206-226 (apply_rope) dispatches to.
+ * q (B, T, Hq, D), k (B, T, Hkv, D), f16|bf16|f32, same dtype, D even; each
+ * is read as B*T rows through one row stride (head_dim unit-stride, heads D
+ * apart, stride(0) == T*stride(1) unless T == 1), so the Q/K slices of a
+ * fused qkv buffer need no copy.  cos, sin (Tc, D) duplicated or (Tc, D/2)
+ * raw, f16|bf16|f32, unit-stride rows; only the first D/2 columns are read;
+ * row r of q/k uses position r % Tc.  interleaved 0: pairs (i, i + D/2)
+ * (Llama/NeoX), 1: pairs (2i, 2i + 1) (GPT-J).  q_out, k_out contiguous,
+ * the inputs' shape and dtype.  out_a = x_a cos - x_b sin and
+ * out_b = x_b cos + x_a sin in fp32 with each product rounded (no fused
+ * multiply-add), then rounded to the output dtype (nearest even). */
+int sia_rope_qk(const sia_tensor* q, const sia_tensor* k, const sia_tensor* cos, const sia_tensor* sin,
+                int32_t interleaved, const sia_tensor* q_out, const sia_tensor* k_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

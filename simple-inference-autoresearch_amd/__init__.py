@@ -26,6 +26,7 @@ from .decode import (
 from .prefill import attention_flash_triton, prefill_workspace_size
 from .kv_cache import KVCache, kv_write, quantize_kv_int8
 from .paged_kv_cache import PagedKVCache
+from .rope import RopeFrequencies, apply_rope, rope_triton
 from .attention import DecodeCtx, decode_step_attention, gqa_attention
 from . import plugins  # noqa: F401  (cache builders, transformers attention hook)
 
@@ -34,6 +35,9 @@ __all__ = [
     "KVCache",
     "LibraryMissing",
     "PagedKVCache",
+    "RopeFrequencies",
+    "apply_rope",
+    "rope_triton",
     "decode_step_attention",
     "gqa_attention",
     "kv_write",

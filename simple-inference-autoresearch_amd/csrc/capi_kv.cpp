@@ -51,13 +51,6 @@ int check_scale(const sia_tensor* s, const sia_tensor* like, const char* name) {
   return SIA_OK;
 }
 
-int device_ok() {
-  const DeviceInfo& dev = device_info();
-  if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
-  if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
-  return SIA_OK;
-}
-
 }  // namespace
 
 extern "C" {

@@ -22,6 +22,14 @@ struct DeviceInfo {
 // Facts about the current device (cached per device id).
 const DeviceInfo& device_info();
 
+// SIA_OK when the current device is a gfx950, else a SIA_ERR_DEVICE failure.
+inline int device_ok() {
+  const DeviceInfo& dev = device_info();
+  if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
+  if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
+  return SIA_OK;
+}
+
 // Active work-groups per CU for a kernel at a block size and dynamic LDS size
 // (cached; computed with hipOccupancyMaxActiveBlocksPerMultiprocessor).
 int kernel_occupancy(const void* kernel, int block, size_t lds);

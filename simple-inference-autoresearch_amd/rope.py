@@ -1,0 +1,153 @@
+"""Rotary position embedding with the reference's interface.
+
+Drop-in for ``kernels/rope_kernel.py`` and ``ops/rope.py`` of the reference
+engine:
+
+* :func:`rope_triton` -- ``kernels/rope_kernel.py:261-285`` (and
+  ``_check_cos_sin`` / ``_apply_qk``, 167-258): Q and K rotated in one HIP
+  launch (``sia_rope_qk``), strided Q/K slices of a fused qkv buffer read
+  without a copy, contiguous outputs.
+* :func:`apply_rope` -- ``ops/rope.py:206-226``: the split-half rotation the
+  attention module calls.
+* :class:`RopeFrequencies` -- ``ops/rope.py:72-185``: the cos/sin tables
+  (Llama 3 frequency scaling) and their per-dtype cast cache.
+
+The rotation is ``out_a = x_a cos - x_b sin``, ``out_b = x_b cos + x_a sin``
+in fp32 with every product and sum rounded on its own (no fused
+multiply-add), stored in the input dtype with round-to-nearest-even.  Row
+``r`` of the flattened ``(B*T)`` rows takes position ``r % cos.shape[0]``,
+as in the reference kernel.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+
+def _check_cos_sin(cos: torch.Tensor, sin: torch.Tensor, head_dim: int) -> int:
+    """The reference's table checks (``kernels/rope_kernel.py:167-190``); returns the row stride."""
+    half = head_dim // 2
+    if cos.shape[-1] not in (head_dim, half):
+        raise ValueError(f"cos/sin last dim must be head_dim ({head_dim}) or head_dim/2 ({half}); "
+                         f"got {cos.shape[-1]}")
+    if cos.shape != sin.shape:
+        raise ValueError(f"cos and sin must have identical shape; got {cos.shape} vs {sin.shape}")
+    if cos.stride(-1) != 1 or sin.stride(-1) != 1:
+        raise ValueError("cos/sin must be unit-stride along the last dim")
+    if cos.stride(0) != sin.stride(0):
+        raise ValueError("cos and sin must share the same row stride")
+    if cos.dim() != 2:
+        raise ValueError(f"cos/sin must be (seq_len, width) tables; got {cos.dim()} dims")
+    return cos.stride(0)
+
+
+def _row_stride(x: torch.Tensor, T: int, head_dim: int):
+    """Stride between the flattened ``B*T`` rows of ``x``, or None when rows are not uniformly spaced.
+
+    A size-1 dim's stride is never used (torch calls such views contiguous
+    whatever that stride is).
+    """
+    if x.stride(-1) != 1 or (x.shape[2] > 1 and x.stride(2) != head_dim):
+        return None
+    if T == 1:
+        return x.stride(0)
+    if x.shape[0] == 1 or x.stride(0) == T * x.stride(1):
+        return x.stride(1)
+    return None
+
+
+def rope_triton(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                interleaved: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rotate ``q (B, T, Hq, D)`` and ``k (B, T, Hkv, D)`` by the ``cos``/``sin`` tables.
+
+    ``cos``/``sin``: ``(T', D)`` duplicated or ``(T', D/2)`` raw; only the
+    first ``D/2`` columns are read.  ``interleaved=False`` pairs ``(i, i+D/2)``
+    (Llama/NeoX), ``True`` pairs ``(2i, 2i+1)`` (GPT-J).  Returns contiguous
+    ``(q_rot, k_rot)`` with the inputs' shapes and dtypes.
+    """
+    head_dim = q.shape[-1]
+    _check_cos_sin(cos, sin, head_dim)
+    B, T, n_heads_q, head_dim = q.shape
+    if head_dim % 2:
+        raise AssertionError("head_dim must be even for RoPE")
+    if not (k.shape[0] == B and k.shape[1] == T and k.shape[3] == head_dim):
+        raise AssertionError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)} in B, T or head_dim")
+    if sin.shape[0] != cos.shape[0]:
+        raise AssertionError("cos and sin must have the same number of rows")
+    if not (q.is_cuda and k.is_cuda and cos.is_cuda and sin.is_cuda):
+        raise ValueError("rope_triton runs on the GPU: q, k, cos and sin must be CUDA (HIP) tensors")
+    h = _lib.require_library()
+    if _row_stride(q, T, head_dim) is None:
+        q = q.contiguous()
+    if _row_stride(k, T, head_dim) is None:
+        k = k.contiguous()
+    q_out = torch.empty(B, T, n_heads_q, head_dim, dtype=q.dtype, device=q.device)
+    k_out = torch.empty(B, T, k.shape[2], head_dim, dtype=k.dtype, device=k.device)
+    descs = [ctypes.byref(_lib.desc(t)) for t in (q, k, cos, sin)]
+    with torch.cuda.device(q.device):
+        rc = h.sia_rope_qk(*descs, ctypes.c_int32(1 if interleaved else 0), ctypes.byref(_lib.desc(q_out)),
+                           ctypes.byref(_lib.desc(k_out)), ctypes.c_void_p(_lib.stream_handle(q.device)))
+    _lib.check(rc)
+    return q_out, k_out
+
+
+def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """``ops/rope.py:206``: split-half RoPE of ``q``/``k`` with ``(T, head_dim)`` tables."""
+    return rope_triton(q, k, cos, sin)
+
+
+class RopeFrequencies:
+    """cos/sin tables for positions ``[0, max_seq_len)`` (``ops/rope.py:72-185``).
+
+    Frequencies ``1 / theta^(2i/D)`` in fp32; with ``rope_type="llama3"`` each
+    is rescaled by wavelength (kept below ``original_max_seq_len /
+    high_freq_factor``, divided by ``factor`` above ``original_max_seq_len /
+    low_freq_factor``, linearly blended between), the blend evaluated in
+    double precision as the reference does, then stored as fp32.  Tables are
+    fp32 ``(max_seq_len, head_dim)`` with each angle duplicated across the
+    two halves.
+    """
+
+    def __init__(self, head_dim: int, max_seq_len: int, rope_theta: float = 500_000.0, rope_type: str = "llama3",
+                 factor: float = 32.0, low_freq_factor: float = 1.0, high_freq_factor: float = 4.0,
+                 original_max_seq_len: int = 8192, device: torch.device | None = None):
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+        device = device or torch.device("cuda" if torch.cuda.is_available() else "cpu")
+        exponent = torch.arange(0, head_dim, 2, dtype=torch.float32, device=device) / head_dim
+        freqs = 1.0 / (rope_theta ** exponent)
+        if rope_type == "llama3":
+            freqs = self._llama3_scaled(freqs, factor, low_freq_factor, high_freq_factor, original_max_seq_len)
+        angle = torch.outer(torch.arange(max_seq_len, dtype=torch.float32, device=device), freqs)
+        angle = torch.cat([angle, angle], dim=-1)
+        self.cos = angle.cos()
+        self.sin = angle.sin()
+        self._cast_cache: dict[torch.dtype, tuple[torch.Tensor, torch.Tensor]] = {}
+
+    @staticmethod
+    def _llama3_scaled(freqs: torch.Tensor, factor: float, low_freq_factor: float, high_freq_factor: float,
+                       original_max_seq_len: int) -> torch.Tensor:
+        f = freqs.double()
+        wavelen = (2 * math.pi) / f
+        smooth = (original_max_seq_len / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor)
+        blended = (1 - smooth) * f / factor + smooth * f
+        out = torch.where(wavelen > original_max_seq_len / low_freq_factor, f / factor, blended)
+        out = torch.where(wavelen < original_max_seq_len / high_freq_factor, f, out)
+        return out.to(freqs.dtype)
+
+    def get(self, seq_len: int, start_pos: int = 0, dtype: torch.dtype | None = None):
+        """``(cos, sin)`` rows ``[start_pos, start_pos + seq_len)``, cast to ``dtype`` from a cached full table."""
+        if dtype is None or dtype == torch.float32:
+            cos_tbl, sin_tbl = self.cos, self.sin
+        else:
+            cached = self._cast_cache.get(dtype)
+            if cached is None:
+                cached = (self.cos.to(dtype), self.sin.to(dtype))
+                self._cast_cache[dtype] = cached
+            cos_tbl, sin_tbl = cached
+        return cos_tbl[start_pos:start_pos + seq_len], sin_tbl[start_pos:start_pos + seq_len]
