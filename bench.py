@@ -248,6 +248,84 @@ def bench_rope_config(pkg, steps: int, warmup: int):
         out[label] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(gbs, 1),
                       "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
     out["workload"] = "fused q/k RoPE bf16, 32/8 heads D128, split-half, Llama 3 tables"
+    out["rope_kv_write"] = bench_rope_kv_write(pkg, rf, steps, warmup)
+    return out
+
+
+def rope_kv_write_bytes(B: int, T: int, Hq: int, Hkv: int, D: int) -> int:
+    """Algorithmic bytes of one fused RoPE + int8 KV write (bf16 q/k/v, bf16 tables, int8 K/V with
+    fp32 scales): read q, k, v and half a cos and a sin row per token; write q_rot, the int8 K/V
+    rows and their scales."""
+    per_token = (Hq + 2 * Hkv) * D * 2 + 2 * (D // 2) * 2 + Hq * D * 2 + 2 * Hkv * D + 2 * Hkv * 4
+    return B * T * per_token
+
+
+def bench_rope_kv_write(pkg, rf, steps: int, warmup: int):
+    """RoPE of q and k fused into the int8 cache write (one launch), against the reference's order
+    (RoPE launch, then the write) on the same inputs: prefill B1 T8192 into a contiguous int8 cache,
+    and a B64 decode step into paged int8 pools at per-sequence positions."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D = 32, 8, 128
+    cos, sin = rf.get(8192, dtype=torch.bfloat16)
+    out = {}
+    for label, B, T in (("prefill_B1_T8192", 1, 8192), ("decode_B64_T1", 64, 1)):
+        g = torch.Generator(device=dev).manual_seed(9)
+        qkv = torch.randn(B, T, (Hq + 2 * Hkv) * D, device=dev, dtype=torch.bfloat16, generator=g)
+        q = qkv[..., :Hq * D].view(B, T, Hq, D)
+        k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, T, Hkv, D)
+        v = qkv[..., (Hq + Hkv) * D:].view(B, T, Hkv, D)
+        if T > 1:
+            kc = torch.zeros(B, Hkv, 8192, D, dtype=torch.int8, device=dev)
+            vc = torch.zeros_like(kc)
+            ks = torch.zeros(B, Hkv, 8192, dtype=torch.float32, device=dev)
+            vs = torch.zeros_like(ks)
+            kw = dict(start_offset=0)
+            cs, sn = cos, sin
+        else:
+            pages = B * 512
+            kc = torch.zeros(pages, Hkv, 16, D, dtype=torch.int8, device=dev)
+            vc = torch.zeros_like(kc)
+            ks = torch.zeros(pages, Hkv, 16, dtype=torch.float32, device=dev)
+            vs = torch.zeros_like(ks)
+            bt = torch.randperm(pages, device=dev, generator=g).int().view(B, 512)
+            pos = torch.randint(1, 8192, (B,), device=dev, generator=g).int()
+            kw = dict(block_table=bt, start_pos=pos, start_offset=-1, page_size=16)
+            cs, sn = cos, sin
+        q_out = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=dev)
+
+        def fused():
+            pkg.rope_kv_write(q, k, v, cs, sn, kc, vc, ks, vs, q_out=q_out, **kw)
+
+        def unfused():   # the reference's order; shared position 0.. for prefill, row 4000 for decode
+            if T > 1:
+                qr, kr = pkg.rope_triton(q, k, cos, sin)
+            else:
+                qr, kr = pkg.rope_triton(q, k, cos[4000:4001], sin[4000:4001])
+            pkg.kv_write(kr.transpose(1, 2), v.contiguous().transpose(1, 2), kc, vc, ks, vs, **kw)
+
+        res = {}
+        for name, fn in (("fused", fused), ("rope_then_write", unfused)):
+            settle(fn)
+            for _ in range(warmup):
+                fn()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            res[name] = round(e0.elapsed_time(e1) / steps * 1e3, 2)
+        nbytes = rope_kv_write_bytes(B, T, Hq, Hkv, D)
+        gbs = nbytes / (res["fused"] * 1e-6) / 1e9
+        out[label] = {"fused_us_per_call": res["fused"], "rope_then_write_us_per_call": res["rope_then_write"],
+                      "fused_GBps": round(gbs, 1), "fused_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                      "algorithmic_bytes": nbytes}
+    out["workload"] = ("RoPE of q, k fused into the int8 KV write (bf16 q/k/v slices of one qkv buffer, "
+                       "32/8 heads D128, fp32 scales)")
     return out
 
 

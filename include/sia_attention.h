@@ -188,6 +188,29 @@ int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_d
                  const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst, const sia_tensor* block_table,
                  const sia_tensor* start_pos, int32_t start_pos_host, int32_t page_size, void* stream);
 
+/* RoPE-K fused into the KV write, with q rotated in the same launch.
+ * Replaces the captured decode step's apply_rope + quantize_kv_int8 + four
+ * index_copy_ (ops/attention.py:200-228: rope at 202, writes at 217-228) and
+ * the eager path's apply_rope + KVCache.update (ops/attention.py:290-300);
+ * it is the fused RoPE-K write that model/paged_kv_cache.py:29-30 describes.
+ * q (B, T, Hq, D) or NULL, k and v (B, T, Hkv, D) token-major, as the qkv
+ * projection leaves them (strided slices are read in place); 16-byte aligned
+ * rows.  Token t of sequence b has position p = start_pos_host + start_pos[b]
+ * + t (start_pos as in sia_kv_write) and is rotated by table row p of
+ * cos/sin ((Tc, D) or (Tc, D/2), first D/2 columns read): pairs as in
+ * sia_rope_qk (interleaved 0 or 1), the same fp32 arithmetic.  The rotated K
+ * is rounded to k's dtype, then written like sia_kv_write writes k (cast, or
+ * int8 with a per-token-per-head scale); v is written unrotated; q_out
+ * (B, T, Hq, D), any strides with unit head_dim, receives the rotated q in
+ * q's dtype.  K/V rows whose position is outside the destination or the
+ * table are skipped; q rows whose position is outside the table are written
+ * as zeros. */
+int sia_rope_kv_write(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, const sia_tensor* cos,
+                      const sia_tensor* sin, int32_t interleaved, const sia_tensor* q_out, const sia_tensor* k_dst,
+                      const sia_tensor* v_dst, const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst,
+                      const sia_tensor* block_table, const sia_tensor* start_pos, int32_t start_pos_host,
+                      int32_t page_size, void* stream);
+
 /* Rotary position embedding of Q and K in one launch.  Replaces the Triton
  * kernel _rope_qk_fwd and its wrapper (kernels/rope_kernel.py:86-165,
  * 193-285), which ops/rope.py:206-226 (apply_rope) dispatches to.

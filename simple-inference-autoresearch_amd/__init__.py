@@ -24,10 +24,10 @@ from .decode import (
     paged_gqa_int8_flash_decode,
 )
 from .prefill import attention_flash_triton, prefill_workspace_size
-from .kv_cache import KVCache, kv_write, quantize_kv_int8
+from .kv_cache import KVCache, kv_write, quantize_kv_int8, rope_kv_write
 from .paged_kv_cache import PagedKVCache
 from .rope import RopeFrequencies, apply_rope, rope_triton
-from .attention import DecodeCtx, decode_step_attention, gqa_attention
+from .attention import DecodeCtx, decode_step_attention, gqa_attention, rope_decode_step_attention
 from . import plugins  # noqa: F401  (cache builders, transformers attention hook)
 
 __all__ = [
@@ -37,6 +37,8 @@ __all__ = [
     "PagedKVCache",
     "RopeFrequencies",
     "apply_rope",
+    "rope_decode_step_attention",
+    "rope_kv_write",
     "rope_triton",
     "decode_step_attention",
     "gqa_attention",

@@ -92,6 +92,7 @@ _SIGNATURES = {
     "sia_quantize_kv_int8": [_P, _P, _P, _VP],
     "sia_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _VP],
     "sia_rope_qk": [_P, _P, _P, _P, _I32, _P, _P, _VP],
+    "sia_rope_kv_write": [_P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _VP],
 }
 _STRING_RESULT = {"sia_status_string", "sia_last_error_message"}
 

@@ -13,6 +13,9 @@ those lines, so a caller keeps its own projections and RoPE:
   captured decode step (``ops/attention.py:206-231``) over a contiguous
   :class:`~.kv_cache.KVCache`: int8 caches quantise the new token on the way
   in, and the position and length are read on the device from ``ctx``.
+* :func:`rope_decode_step_attention` -- the same step from the pre-RoPE
+  projections (``ops/attention.py:202-231``): RoPE of q and k fused into the
+  cache write, then attention.
 * :class:`DecodeCtx` -- the device buffers of ``model/cuda_graph_decode.py:53-56``
   (``cos``, ``sin``, ``pos_index``, ``kv_len``), with int32 positions and
   :meth:`DecodeCtx.set_position` for the per-step update
@@ -61,6 +64,28 @@ class DecodeCtx:
         else:
             self.pos_index.fill_(int(pos))
             self.kv_len.fill_(int(pos) + 1)
+
+
+def rope_decode_step_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                               sin: torch.Tensor, kv_cache: KVCache, layer_idx: int, ctx: DecodeCtx,
+                               sm_scale: float | None = None, interleaved: bool = False) -> torch.Tensor:
+    """RoPE, cache write and attention of one decode step: ``q (B, 1, Hq, D)``, ``k, v (B, 1, Hkv, D)``.
+
+    Replaces ``ops/attention.py:202-231`` (``apply_rope`` through the
+    attention call) with two launches: the fused RoPE + K/V write
+    (``sia_rope_kv_write``, which also rotates q) and the decode kernels.
+    ``q, k, v`` are the projections before RoPE, token-major as
+    ``_project_qkv`` returns them; ``cos``/``sin`` are the full tables, read
+    at ``ctx.pos_index`` on the device (``ctx.cos``/``ctx.sin`` are not used).
+    Returns ``(B, 1, Hq, D)``.  Graph safe.
+    """
+    q_rot = kv_cache.write_decode_rope(layer_idx, ctx.pos_index, q, k, v, cos, sin, interleaved=interleaved)
+    B = q.shape[0]
+    kc, vc, ks, vs = kv_cache._layer(layer_idx, B)
+    qh = q_rot.transpose(1, 2)
+    if kv_cache.is_int8:
+        return attention_flash_decode_int8(qh, kc, vc, ks, vs, ctx.kv_len, sm_scale)
+    return attention_flash_decode(qh, kc, vc, ctx.kv_len, sm_scale)
 
 
 def decode_step_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv_cache: KVCache, layer_idx: int,

@@ -51,13 +51,12 @@ int check_scale(const sia_tensor* s, const sia_tensor* like, const char* name) {
   return SIA_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_dst, const sia_tensor* v_dst,
-                 const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst, const sia_tensor* block_table,
-                 const sia_tensor* start_pos, int32_t start_pos_host, int32_t page_size, void* stream) {
+// Validates a KV write of k/v (B, H, T, D) and fills `a` (everything but the
+// RoPE fields); *dst_dtype receives the destination dtype.
+int setup_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_dst, const sia_tensor* v_dst,
+                   const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst, const sia_tensor* block_table,
+                   const sia_tensor* start_pos, int32_t start_pos_host, int32_t page_size, KvWriteArgs& a,
+                   int* dst_dtype) {
   int rc;
   if ((rc = check_rows(k, "k", 16))) return rc;
   if (!src_dtype_ok(k->dtype)) return fail(SIA_ERR_UNSUPPORTED, "k dtype %s: expected float16, bfloat16 or float32",
@@ -102,7 +101,6 @@ int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_d
     return fail(SIA_ERR_UNSUPPORTED, "destination dtype %s not supported", dtype_name(dd));
   }
 
-  KvWriteArgs a;
   memset(&a, 0, sizeof(a));
   if (block_table != nullptr) {
     if (block_table->data == nullptr || block_table->ndim != 2 || block_table->dtype != SIA_I32)
@@ -160,6 +158,90 @@ int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_d
   a.rows = B * H * T;
   a.ntensors = two ? 2 : 1;
   a.amax_floor = amax_floor(k->dtype);
+  *dst_dtype = dd;
+  return SIA_OK;
+}
+
+// (B, T, H, D) viewed as (B, H, T, D): dims 1 and 2 swapped, same memory.
+sia_tensor token_major_as_head_major(const sia_tensor* x) {
+  sia_tensor y = *x;
+  y.shape[1] = x->shape[2]; y.stride[1] = x->stride[2];
+  y.shape[2] = x->shape[1]; y.stride[2] = x->stride[1];
+  return y;
+}
+
+}  // namespace
+
+extern "C" {
+
+int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_dst, const sia_tensor* v_dst,
+                 const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst, const sia_tensor* block_table,
+                 const sia_tensor* start_pos, int32_t start_pos_host, int32_t page_size, void* stream) {
+  KvWriteArgs a;
+  int dd = 0, rc;
+  if ((rc = setup_kv_write(k, v, k_dst, v_dst, k_scale_dst, v_scale_dst, block_table, start_pos, start_pos_host,
+                           page_size, a, &dd)))
+    return rc;
+  return launch_kv_write(a, k->dtype, dd, (hipStream_t)stream);
+}
+
+int sia_rope_kv_write(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, const sia_tensor* cos,
+                      const sia_tensor* sin, int32_t interleaved, const sia_tensor* q_out, const sia_tensor* k_dst,
+                      const sia_tensor* v_dst, const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst,
+                      const sia_tensor* block_table, const sia_tensor* start_pos, int32_t start_pos_host,
+                      int32_t page_size, void* stream) {
+  if (k == nullptr || cos == nullptr || sin == nullptr)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "k, cos and sin are required");
+  if (k->ndim != 4 || (v != nullptr && v->ndim != 4))
+    return fail(SIA_ERR_INVALID_ARGUMENT, "k and v must be (B, T, Hkv, D)");
+  const sia_tensor kh = token_major_as_head_major(k);
+  sia_tensor vh;
+  if (v != nullptr) vh = token_major_as_head_major(v);
+  KvWriteArgs a;
+  int dd = 0, rc;
+  if ((rc = setup_kv_write(&kh, v ? &vh : nullptr, k_dst, v_dst, k_scale_dst, v_scale_dst, block_table, start_pos,
+                           start_pos_host, page_size, a, &dd)))
+    return rc;
+  const int64_t B = k->shape[0], T = k->shape[1], D = k->shape[3];
+  // tables
+  if (cos->data == nullptr || sin->data == nullptr || cos->ndim != 2 || sin->ndim != 2)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos and sin must be (rows, width) tables");
+  if (cos->shape[0] != sin->shape[0] || cos->shape[1] != sin->shape[1])
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos and sin must have identical shape");
+  if (cos->shape[1] != D && cos->shape[1] != D / 2)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin last dim must be head_dim (%lld) or head_dim/2 (%lld)",
+                (long long)D, (long long)(D / 2));
+  if (cos->dtype != sin->dtype || (cos->dtype != SIA_F16 && cos->dtype != SIA_BF16 && cos->dtype != SIA_F32))
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos and sin must share a float dtype");
+  if (cos->stride[1] != 1 || sin->stride[1] != 1 || cos->stride[0] != sin->stride[0])
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin must be unit-stride rows with one row stride");
+  if (cos->shape[0] <= 0 || cos->shape[0] > 0x7fffffff) return fail(SIA_ERR_INVALID_ARGUMENT, "bad table row count");
+  a.rope = interleaved ? 2 : 1;
+  a.cs = (const char*)cos->data;
+  a.sn = (const char*)sin->data;
+  a.tab_rs = cos->stride[0] * elem_size(cos->dtype);
+  a.Tc = (int32_t)cos->shape[0];
+  a.tab_dt = cos->dtype;
+  if (!aligned16(cos->data) || !aligned16(sin->data) || a.tab_rs % 16 != 0)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin must be 16-byte aligned with 16-byte multiple row strides");
+  // q
+  if ((q == nullptr) != (q_out == nullptr)) return fail(SIA_ERR_INVALID_ARGUMENT, "q and q_out go together");
+  if (q != nullptr) {
+    if ((rc = check_rows(q, "q", 16)) || (rc = check_rows(q_out, "q_out", 16))) return rc;
+    if (q->dtype != k->dtype || q_out->dtype != k->dtype)
+      return fail(SIA_ERR_INVALID_ARGUMENT, "q, q_out and k must share a dtype");
+    if (q->shape[0] != B || q->shape[1] != T || q->shape[3] != D)
+      return fail(SIA_ERR_INVALID_ARGUMENT, "q must be (B, T, Hq, D) with k's B, T and D");
+    for (int d = 0; d < 4; ++d)
+      if (q_out->shape[d] != q->shape[d]) return fail(SIA_ERR_INVALID_ARGUMENT, "q_out shape differs from q");
+    if (q->shape[2] > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "too many query heads");
+    a.q = (const char*)q->data;
+    a.qo = (char*)q_out->data;
+    a.q_sb = bstride(q, 0); a.q_st = bstride(q, 1); a.q_sh = bstride(q, 2);
+    a.qo_sb = bstride(q_out, 0); a.qo_st = bstride(q_out, 1); a.qo_sh = bstride(q_out, 2);
+    a.Hq = (int32_t)q->shape[2];
+    a.q_rows = B * q->shape[2] * T;
+  }
   return launch_kv_write(a, k->dtype, dd, (hipStream_t)stream);
 }
 

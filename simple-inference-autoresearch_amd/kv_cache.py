@@ -53,6 +53,36 @@ def kv_write(k: torch.Tensor, v: torch.Tensor | None, k_dst: torch.Tensor, v_dst
     _lib.check(rc)
 
 
+def rope_kv_write(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor | None, cos: torch.Tensor,
+                  sin: torch.Tensor, k_dst: torch.Tensor, v_dst: torch.Tensor | None,
+                  k_scale_dst: torch.Tensor | None = None, v_scale_dst: torch.Tensor | None = None,
+                  block_table: torch.Tensor | None = None, start_pos: torch.Tensor | None = None,
+                  start_offset: int = 0, page_size: int = 0, interleaved: bool = False,
+                  q_out: torch.Tensor | None = None) -> torch.Tensor | None:
+    """RoPE-K fused into the cache write, q rotated in the same launch (``sia_rope_kv_write``).
+
+    ``q (B, T, Hq, D)``, ``k, v (B, T, Hkv, D)``: token-major, as the qkv
+    projection leaves them (strided slices are read in place).  Token ``t`` of
+    sequence ``b`` sits at position ``p = start_offset + start_pos[b] + t`` and
+    is rotated by row ``p`` of the full ``cos``/``sin`` tables.  The rotated K
+    (rounded to k's dtype) and V are written like :func:`kv_write` writes them;
+    the rotated q is returned as ``(B, T, Hq, D)`` (or written to ``q_out``).
+    """
+    h = _lib.require_library()
+    if not k.is_cuda:
+        raise ValueError("rope_kv_write runs on the GPU: k must be a CUDA (HIP) tensor")
+    if q is not None and q_out is None:
+        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    descs = [_desc_or_null(t) for t in (q, k, v, cos, sin)]
+    rest = [_desc_or_null(t) for t in (q_out, k_dst, v_dst, k_scale_dst, v_scale_dst, block_table, start_pos)]
+    with torch.cuda.device(k.device):
+        rc = h.sia_rope_kv_write(*descs, ctypes.c_int32(1 if interleaved else 0), *rest,
+                                 ctypes.c_int32(int(start_offset)), ctypes.c_int32(int(page_size)),
+                                 ctypes.c_void_p(_lib.stream_handle(k.device)))
+    _lib.check(rc)
+    return q_out
+
+
 def quantize_kv_int8(x: torch.Tensor, scale_dtype: torch.dtype = torch.float16):
     """Per-(..., head_dim) symmetric int8 quantisation of a K or V tensor.
 
@@ -152,6 +182,22 @@ class KVCache:
         B = k.shape[0]
         kc, vc, ks, vs = self._layer(layer_idx, B)
         kv_write(k, v, kc, vc, ks, vs, start_pos=_int32_positions(pos_index))
+
+    def write_decode_rope(self, layer_idx: int, pos_index: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                          v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                          interleaved: bool = False) -> torch.Tensor:
+        """RoPE + write of one decode step in one launch; returns the rotated q ``(B, 1, Hq, D)``.
+
+        ``q, k, v``: the projections ``(B, 1, H, D)`` before RoPE
+        (``ops/attention.py:200-202``); ``cos``/``sin``: the full tables
+        (``RopeFrequencies.get(max_seq_len, dtype=...)``), read at each
+        sequence's position ``pos_index`` on the device, so no per-step table
+        row copy is needed.
+        """
+        B = k.shape[0]
+        kc, vc, ks, vs = self._layer(layer_idx, B)
+        return rope_kv_write(q, k, v, cos, sin, kc, vc, ks, vs, start_pos=_int32_positions(pos_index),
+                             interleaved=interleaved)
 
     def reset(self) -> None:
         """Logical reset between independent sequences (nothing to clear, as in the reference)."""

@@ -26,7 +26,7 @@ from __future__ import annotations
 import torch
 
 from .decode import paged_attention_flash_decode, paged_gqa_int8_flash_decode
-from .kv_cache import kv_write
+from .kv_cache import kv_write, rope_kv_write
 
 
 class PagedKVCache:
@@ -113,6 +113,21 @@ class PagedKVCache:
         kp, vp, ks, vs = self.layer(layer_idx)
         kv_write(k, v, kp, vp, ks, vs, block_table=self.block_tables[:B], start_pos=self.seq_lens[:B],
                  start_offset=-1, page_size=self.block_size)
+
+    def write_decode_rope(self, layer_idx: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          cos: torch.Tensor, sin: torch.Tensor, interleaved: bool = False) -> torch.Tensor:
+        """RoPE + paged write of this step's token in one launch; returns the rotated q ``(B, 1, Hq, D)``.
+
+        ``q, k, v``: projections ``(B, 1, H, D)`` before RoPE.  Request ``b``'s
+        token sits at position ``seq_lens[b] - 1`` (read on the device) and is
+        rotated by that row of the full ``cos``/``sin`` tables, so requests at
+        different positions share one launch.
+        """
+        B = k.shape[0]
+        kp, vp, ks, vs = self.layer(layer_idx)
+        return rope_kv_write(q, k, v, cos, sin, kp, vp, ks, vs, block_table=self.block_tables[:B],
+                             start_pos=self.seq_lens[:B], start_offset=-1, page_size=self.block_size,
+                             interleaved=interleaved)
 
     def decode_attention(self, layer_idx: int, q: torch.Tensor, sm_scale: float | None = None) -> torch.Tensor:
         """Decode attention of ``q (B, Hq, 1, D)`` over each request's ``seq_lens[b]`` cached tokens."""
