@@ -291,3 +291,107 @@ def test_invalid_arguments(gpu_pkg):
         gpu_pkg.rope_kv_write(q, k, v, cos[:, :20], sin[:, :20], kc, torch.zeros_like(kc))
     with pytest.raises(ValueError, match="share a dtype"):
         gpu_pkg.rope_kv_write(q.float(), k, v, cos, sin, kc, torch.zeros_like(kc))
+
+
+def test_rope_decode_step_hip_graph_contiguous(gpu_pkg):
+    """ops/attention.py:180-245 as one captured graph: fused RoPE + int8 write + attention,
+    replayed at new per-sequence positions (ctx filled between replays, as
+    model/cuda_graph_decode.py:98-102 does); every replay equals the eager unfused step."""
+    B, Hq, Hkv, D, S = 3, 32, 8, 128, 600
+    announce("rope_decode_step_attention in a HIP graph (contiguous int8 cache)")
+    torch.manual_seed(31)
+    cg = gpu_pkg.KVCache(1, B, S, Hkv, D, device=DEV)
+    ce = gpu_pkg.KVCache(1, B, S, Hkv, D, device=DEV)
+    pre_k = torch.randn(B, Hkv, S, D, device=DEV).to(torch.bfloat16)
+    pre_v = torch.randn(B, Hkv, S, D, device=DEV).to(torch.bfloat16)
+    for c in (cg, ce):
+        c.update(0, 0, pre_k, pre_v)
+    rf = gpu_pkg.RopeFrequencies(D, S, device=torch.device(DEV))
+    cos, sin = rf.get(S, dtype=torch.bfloat16)
+    ctx = gpu_pkg.DecodeCtx(D, DEV, batch=B, per_sequence=True)
+    qkv = torch.zeros(B, 1, (Hq + 2 * Hkv) * D, dtype=torch.bfloat16, device=DEV)
+    q = qkv[..., :Hq * D].view(B, 1, Hq, D)
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].view(B, 1, Hkv, D)
+    v = qkv[..., (Hq + Hkv) * D:].view(B, 1, Hkv, D)
+    ctx.set_position(torch.tensor([10, 20, 30], dtype=torch.int32, device=DEV))
+    gpu_pkg.rope_decode_step_attention(q, k, v, cos, sin, cg, 0, ctx)      # warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = gpu_pkg.rope_decode_step_attention(q, k, v, cos, sin, cg, 0, ctx)
+    torch.cuda.synchronize()
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    for i, pos in enumerate(([10, 20, 30], [11, 200, 31], [12, 201, 599], [400, 7, 0])):
+        pt = torch.tensor(pos, dtype=torch.int32, device=DEV)
+        ctx.set_position(pt)
+        qkv.copy_(torch.randn(qkv.shape, generator=gen, device=DEV))
+        g.replay()
+        torch.cuda.synchronize()
+        # eager, unfused: per-sequence RoPE with the reference kernel's interface, then write + attend
+        qr = torch.empty_like(q)
+        kr = torch.empty_like(k)
+        for b, p in enumerate(pos):
+            qr[b:b + 1], kr[b:b + 1] = gpu_pkg.rope_triton(q[b:b + 1], k[b:b + 1], cos[p:p + 1], sin[p:p + 1])
+        ref = gpu_pkg.decode_step_attention(qr.transpose(1, 2), kr.transpose(1, 2), v.contiguous().transpose(1, 2),
+                                            ce, 0, ctx)
+        torch.cuda.synchronize()
+        assert torch.equal(cg.k_cache, ce.k_cache) and torch.equal(cg.v_cache, ce.v_cache), f"replay {i}"
+        assert torch.equal(cg.k_scale, ce.k_scale) and torch.equal(cg.v_scale, ce.v_scale), f"replay {i}"
+        assert torch.equal(out, ref), f"replay {i}"
+
+
+def test_rope_paged_decode_step_hip_graph(gpu_pkg):
+    """Paged pools with per-sequence seq_lens: begin_decode_step + write_decode_rope +
+    decode_attention captured once and replayed; each replay equals the eager unfused step."""
+    B, Hq, Hkv, D, bs = 3, 16, 4, 128, 16
+    announce("paged rope decode step in a HIP graph")
+    torch.manual_seed(41)
+    caches = [gpu_pkg.PagedKVCache(1, B, 256, Hkv, D, block_size=bs, device=DEV, kv_dtype=torch.int8)
+              for _ in range(2)]
+    k0 = torch.randn(B, Hkv, 100, D, device=DEV).to(torch.bfloat16)
+    v0 = torch.randn(B, Hkv, 100, D, device=DEV).to(torch.bfloat16)
+    for c in caches:
+        c.allocate(B, c.max_blocks_per_seq)
+        c.write_prefill(0, B, k0, v0)
+    lens0 = torch.tensor([5, 50, 100], dtype=torch.int32, device=DEV)
+    rf = gpu_pkg.RopeFrequencies(D, 256, device=torch.device(DEV))
+    cos, sin = rf.get(256, dtype=torch.bfloat16)
+    q = torch.zeros(B, 1, Hq, D, dtype=torch.bfloat16, device=DEV)
+    k = torch.zeros(B, 1, Hkv, D, dtype=torch.bfloat16, device=DEV)
+    v = torch.zeros(B, 1, Hkv, D, dtype=torch.bfloat16, device=DEV)
+    cg, ce = caches
+
+    def step():
+        cg.begin_decode_step(B)
+        q_rot = cg.write_decode_rope(0, q, k, v, cos, sin)
+        return cg.decode_attention(0, q_rot.transpose(1, 2))
+
+    cg.seq_lens[:B].copy_(lens0)
+    step()                                        # warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = step()
+    torch.cuda.synchronize()
+    cg.seq_lens[:B].copy_(lens0)
+    ce.seq_lens[:B].copy_(lens0)
+    gen = torch.Generator(device=DEV).manual_seed(6)
+    for i in range(4):
+        q.copy_(torch.randn(q.shape, generator=gen, device=DEV))
+        k.copy_(torch.randn(k.shape, generator=gen, device=DEV))
+        v.copy_(torch.randn(v.shape, generator=gen, device=DEV))
+        g.replay()
+        torch.cuda.synchronize()
+        ce.begin_decode_step(B)
+        pos = [int(n) - 1 for n in ce.seq_lens[:B].tolist()]
+        qr = torch.empty_like(q)
+        kr = torch.empty_like(k)
+        for b, p in enumerate(pos):
+            qr[b:b + 1], kr[b:b + 1] = gpu_pkg.rope_triton(q[b:b + 1], k[b:b + 1], cos[p:p + 1], sin[p:p + 1])
+        ce.write_decode(0, kr.transpose(1, 2), v.transpose(1, 2))
+        ref = ce.decode_attention(0, qr.transpose(1, 2))
+        torch.cuda.synchronize()
+        assert cg.seq_lens[:B].tolist() == ce.seq_lens[:B].tolist() == [n + i + 1 for n in (5, 50, 100)]
+        assert torch.equal(cg.k_pool, ce.k_pool) and torch.equal(cg.k_scale_pool, ce.k_scale_pool), f"replay {i}"
+        assert torch.equal(cg.v_pool, ce.v_pool), f"replay {i}"
+        assert torch.equal(out, ref), f"replay {i}"
