@@ -99,7 +99,8 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   p.vimg = (char*)workspace;
   p.Hkv = (int)Hkv; p.Tk = (int)Tk; p.nkb = a.nkb;
   p.nblocks = B * Hkv * a.nkb;
-  if (p.nblocks * (D < 32 ? 32 : D) / 256 + 1 > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "K/V too large");
+  // one work-group per image (grid x dimension), 32-bit indexed in the kernel
+  if (p.nblocks > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "K/V too large");
   L.D = (int)D;
   L.dtype = q->dtype;
   L.stream = (hipStream_t)stream;

@@ -8,9 +8,8 @@ namespace sia {
 template <int D, class T>
 static int launch_prefill_typed(PrefillLaunch& L) {
   if (L.pack.nblocks > 0) {
-    const int64_t threads = L.pack.nblocks * PfCfg<D>::DV;   // one thread per (image chunk, 8 dims)
-    hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, L.stream,
-                       L.pack);
+    // one work-group per 64-key V^T image
+    hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)L.pack.nblocks), dim3(256), 0, L.stream, L.pack);
   }
   const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
   hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(PfCfg<D>::waves * 64), 0, L.stream, L.a);

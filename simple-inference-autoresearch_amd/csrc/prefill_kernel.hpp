@@ -105,48 +105,63 @@ inline int pf_rows_per_group(int D) { return D <= 128 ? 256 : 128; }
 // of half c%2, i.e. 4 (c%2) + {0, 1, 2, 3, 8, 9, 10, 11}.
 __device__ __forceinline__ int image_key(int c, int i) { return 16 * (c >> 1) + 4 * (c & 1) + (i & 3) + 8 * (i >> 2); }
 
-// Element `hs` (0 low, 1 high) of two packed 16-bit words as one f16 pair.
-// bf16 sources are widened to f32, clamped to the f16 range and rounded: the
-// PV product runs in f16 so that P keeps 11 significant bits.
-__device__ __forceinline__ uint32_t to_f16_pair(F16, uint32_t a, uint32_t b, int hs) { return gather16(a, b, hs); }
-__device__ __forceinline__ uint32_t to_f16_pair(BF16, uint32_t a, uint32_t b, int hs) {
-  const float fa = __builtin_bit_cast(float, hs ? (a & 0xffff0000u) : (a << 16));
-  const float fb = __builtin_bit_cast(float, hs ? (b & 0xffff0000u) : (b << 16));
-  return pack2(F16{}, __builtin_amdgcn_fmed3f(fa, -65504.0f, 65504.0f),
-               __builtin_amdgcn_fmed3f(fb, -65504.0f, 65504.0f));
+// One 16-bit V element (raw bits) as f16 bits: bf16 is widened to f32,
+// clamped to the f16 range and rounded (the PV product runs in f16 so that P
+// keeps 11 significant bits).
+__device__ __forceinline__ uint32_t elem_f16(F16, uint32_t bits) { return bits; }
+__device__ __forceinline__ uint32_t elem_f16(BF16, uint32_t bits) {
+  const float f = __builtin_amdgcn_fmed3f(__builtin_bit_cast(float, bits << 16), -65504.0f, 65504.0f);
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
 
-// V (B, Hkv, Tk, D) -> images [B][Hkv][nkb]: image chunk c of dimension d
-// (16 bytes at (c * DV + d) * 16) holds keys image_key(c, 0..7) of d as f16;
-// keys at or past Tk and dimensions past D are zero.  One thread makes 8 (d)
-// x 8 (keys).
+// V (B, Hkv, Tk, D) -> images [B][Hkv][nkb]: image chunk x = c * DV + d (16
+// bytes at x * 16) holds keys image_key(c, 0..7) of dimension d as f16; keys
+// at or past Tk and dimensions past D are zero.  One work-group per image:
+// the 64 x D block is read with coalesced 16-byte loads into LDS (rows padded
+// by 8 bytes so the 8 rows one output chunk gathers sit in different banks),
+// then every thread assembles whole output chunks, so each store instruction
+// of a wave writes one contiguous 1 KB run.
 template <int D, class T>
 __global__ __launch_bounds__(256) void prefill_pack_v(const PackArgs a) {
   constexpr int DV = PfCfg<D>::DV;
-  constexpr int DG = DV / 8;
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t blk = gid / (8 * DG);
-  if (blk >= a.nblocks) return;
-  const int r = (int)(gid % (8 * DG));
-  const int c = r / DG, dg = r % DG;
-  const int kb = (int)(blk % a.nkb);
-  const int64_t bh = blk / a.nkb;
-  const int hkv = (int)(bh % a.Hkv);
-  const int64_t b = bh / a.Hkv;
-  const char* src = a.v + b * a.v_sb + (int64_t)hkv * a.v_sh + dg * 16;
-  u32x4 in[8];
+  constexpr int RS = D + 4;                       // LDS row stride in 16-bit elements
+  constexpr int IN = kPfBN * D / 8;               // 16-byte input chunks per block
+  constexpr int OUT = 8 * DV;                     // 16-byte output chunks per image
+  __shared__ __attribute__((aligned(16))) uint16_t tile[kPfBN * RS];
+  const uint32_t blk = blockIdx.x;
+  const uint32_t bh = blk / (uint32_t)a.nkb;
+  const int kb = (int)(blk - bh * (uint32_t)a.nkb);
+  const uint32_t b = bh / (uint32_t)a.Hkv;
+  const int hkv = (int)(bh - b * (uint32_t)a.Hkv);
+  const char* src = a.v + (int64_t)b * a.v_sb + (int64_t)hkv * a.v_sh;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int key = kb * kPfBN + image_key(c, i);
-    in[i] = key < a.Tk && 8 * dg < D ? *(const u32x4*)(src + (int64_t)key * a.v_sn) : u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < (IN + 255) / 256; ++i) {
+    const int q = threadIdx.x + 256 * i;
+    if (q < IN) {
+      const int row = q / (D / 8), c8 = q % (D / 8);
+      const int key = kb * kPfBN + row;
+      const u32x4 w = key < a.Tk ? *(const u32x4*)(src + (int64_t)key * a.v_sn + c8 * 16) : u32x4{0u, 0u, 0u, 0u};
+      uint32_t* t = (uint32_t*)(tile + row * RS + c8 * 8);   // 8-byte aligned (RS * 2 % 8 == 0)
+      *(u32x2*)t = u32x2{w[0], w[1]};
+      *(u32x2*)(t + 2) = u32x2{w[2], w[3]};
+    }
   }
-  char* dst = a.vimg + blk * PfCfg<D>::vblk + (int64_t)(c * DV + 8 * dg) * 16;
+  __syncthreads();
+  char* dst = a.vimg + (int64_t)blk * PfCfg<D>::vblk;
 #pragma unroll
-  for (int x = 0; x < 8; ++x) {
-    u32x4 w;
+  for (int i = 0; i < OUT / 256; ++i) {
+    const int x = threadIdx.x + 256 * i;
+    const int c = x / DV, d = x % DV;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (d < D) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) w[m] = to_f16_pair(T{}, in[2 * m][x >> 1], in[2 * m + 1][x >> 1], x & 1);
-    *(u32x4*)(dst + 16 * x) = w;
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t lo = elem_f16(T{}, tile[image_key(c, 2 * m) * RS + d]);
+        const uint32_t hi = elem_f16(T{}, tile[image_key(c, 2 * m + 1) * RS + d]);
+        w[m] = lo | (hi << 16);
+      }
+    }
+    *(u32x4*)(dst + (int64_t)x * 16) = w;
   }
 }
 
