@@ -329,6 +329,58 @@ def bench_rope_kv_write(pkg, rf, steps: int, warmup: int):
     return out
 
 
+def _time_calls(fn, steps: int, warmup: int) -> float:
+    """Mean milliseconds per call of `fn` over `steps` back-to-back calls (after settle + warm-up)."""
+    import torch
+
+    settle(fn)
+    for _ in range(warmup):
+        fn()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_qwen35_config(pkg, steps: int, warmup: int):
+    """Qwen3.5 full-attention shapes (head_dim 256, 16 query / 4 KV heads, bf16), the path the
+    transformers attention hook takes: decode B32 over a contiguous 4096-token cache
+    (attention_flash_decode) and a causal prefill of 4096 tokens (attention_flash_triton)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(11)
+    Hq, Hkv, D = 16, 4, 256
+    out = {}
+    B, S = 32, 4096
+    q = torch.randn(B, Hq, 1, D, device=dev, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+    kv_len = torch.tensor([S], dtype=torch.int32, device=dev)
+    ms = _time_calls(lambda: pkg.attention_flash_decode(q, k, v, kv_len), steps, warmup)
+    nbytes = 2 * B * Hkv * S * D * 2 + 2 * B * Hq * D * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out["decode_B32_ctx4096"] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+                                 "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+    del q, k, v
+    T = 4096
+    q = (torch.randn(1, Hq, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    ms = _time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True), steps, warmup)
+    flops = _syn().prefill_flops(1, Hq, T, D)
+    tf = flops / (ms * 1e-3) / 1e12
+    out["prefill_B1_T4096"] = {"us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                               "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": flops}
+    out["workload"] = "Qwen3.5 full attention: head_dim 256, 16/4 heads, bf16, contiguous cache"
+    return out
+
+
 def bench_copy(steps: int, warmup: int, nbytes: int = 1 << 30):
     """A plain device-to-device copy of `nbytes` (torch's copy kernel).
 
@@ -373,8 +425,8 @@ def main(argv=None):
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--settle-ms", type=float, default=300.0,
                    help="untimed back-to-back calls before each config's warm-up, so the GPU clocks settle")
-    p.add_argument("--no-others", action="store_true", help="skip configs 2, 4, 5 and the RoPE lines")
-    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "rope", "copy"],
+    p.add_argument("--no-others", action="store_true", help="skip configs 2, 4, 5, the RoPE and the Qwen3.5 lines")
+    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "rope", "qwen35", "copy"],
                    help="config to run alone (profiling runs); 'copy' is a plain 1 GiB device copy "
                         "that calibrates the HBM byte counters")
     args = p.parse_args(argv)
@@ -398,6 +450,10 @@ def main(argv=None):
     if args.config == "copy":   # counter calibration: 1 GiB read + 1 GiB written per launch
         r = bench_copy(args.steps, args.warmup)
         print(json.dumps({"config": "copy", **r}), flush=True)
+        return 0
+    if args.config == "qwen35":   # Qwen3.5 attention shapes only (profiling runs)
+        r = bench_qwen35_config(pkg, args.steps, args.warmup)
+        print(json.dumps({"config": "qwen35", **r}), flush=True)
         return 0
     if args.config == "rope":   # fused RoPE only (profiling runs)
         r = bench_rope_config(pkg, args.steps, args.warmup)
@@ -469,6 +525,8 @@ def main(argv=None):
         print(f"[bench] cfg4: {others['cfg4']}", file=sys.stderr, flush=True)
         others["rope"] = bench_rope_config(pkg, max(20, args.steps // 2), args.warmup)
         print(f"[bench] rope: {others['rope']}", file=sys.stderr, flush=True)
+        others["qwen35"] = bench_qwen35_config(pkg, max(20, args.steps // 2), args.warmup)
+        print(f"[bench] qwen35: {others['qwen35']}", file=sys.stderr, flush=True)
         result["other_configs"] = others
         case = None
 

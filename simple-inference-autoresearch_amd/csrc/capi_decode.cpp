@@ -21,8 +21,8 @@ struct Geometry {
 };
 
 size_t plan_bytes(int B) { return (size_t)round_up((int64_t)(kPlanHeader + B + 1) * 4, 256); }
-// One item holds a partial for each of its kDecodeWaves unit slots.
-size_t item_bytes(const Geometry& g) { return (size_t)kDecodeWaves * g.G16 * (g.D + 2) * 4; }
+// One item holds a partial for each of its decode_waves(D) unit slots.
+size_t item_bytes(const Geometry& g) { return (size_t)decode_waves(g.D) * g.G16 * (g.D + 2) * 4; }
 
 // Partial slots the workspace must hold: two per persistent work-group (its
 // first and last segment may each be a piece of a split sequence), for up to
@@ -43,7 +43,8 @@ int geometry(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, Geometry& g) {
   g.G = (int)(Hq / Hkv);
   g.HG = (g.G + 15) / 16;
   g.U = g.Hkv * g.HG;
-  g.UB = g.U >= kDecodeWaves ? (g.U + kDecodeWaves - 1) / kDecodeWaves : 1;
+  const int nw = decode_waves(g.D);
+  g.UB = g.U >= nw ? (g.U + nw - 1) / nw : 1;
   g.G16 = g.G < 16 ? g.G : 16;
   return SIA_OK;
 }
@@ -208,7 +209,7 @@ int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decod
   a.ws_plan = (int32_t*)ws;
   a.max_items = (int32_t)items;
   a.ws_ml = (float*)((char*)ws + pb);
-  a.ws_acc = a.ws_ml + (size_t)items * kDecodeWaves * g.G16 * 2;
+  a.ws_acc = a.ws_ml + (size_t)items * decode_waves(g.D) * g.G16 * 2;
   a.tps_force = opts ? opts->tiles_per_split : 0;
   return SIA_OK;
 }

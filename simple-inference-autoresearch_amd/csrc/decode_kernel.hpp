@@ -197,7 +197,13 @@ __device__ __forceinline__ int sk_group(int x, int W, int G) {
 // One 16-token tile's operands as held by one lane.
 template <int D, class KV, class ST>
 struct Tile {
-  static constexpr int KB = (D / 4) * KV::bytes;     // K bytes per lane: token lane16, elems [grp*D/4, +D/4)
+  // K bytes per lane, token lane16.  16-bit K: 16 bytes per k-step j at
+  // elements [32 j + 8 grp, +8), the MFMA operand's own order, so the 4 lanes
+  // of a row read 64 contiguous bytes per load instruction (16 cache lines
+  // per instruction instead of 64).  int8 K: elements [grp*D/4, +D/4), one
+  // contiguous run (a 128-byte row is already one line per instruction).
+  static constexpr int KB = (D / 4) * KV::bytes;
+  static constexpr int KSTRIDE = std::is_same<KV, I8>::value ? 16 : 64;   // bytes between a lane's K pieces
   static constexpr int VB = (D / 16) * KV::bytes;    // V bytes per lane per token: elems [lane16*D/16, +D/16)
   static constexpr bool kInt8 = std::is_same<KV, I8>::value;
   Raw<KB> k;
@@ -205,8 +211,8 @@ struct Tile {
   float ks[4], vs[4];                                // int8 scales of tokens 4*grp + i
 };
 
-// This lane's byte offsets inside one tile (constant): K of token lane16,
-// elements [grp*D/4, +D/4); V of token 4*grp+i, elements [lane16*D/16,
+// This lane's byte offsets inside one tile (constant): K of token lane16
+// (its first piece; see Tile); V of token 4*grp+i, elements [lane16*D/16,
 // +D/16); the scales of tokens 4*grp .. 4*grp+3.
 struct LaneOff {
   uint32_t k;
@@ -228,13 +234,14 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const char* p) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, 0, -1, kRawBufferFlags);
 }
 
-// BYTES at rsrc + off (BYTES a multiple of 16, or 8 or 4).
-template <int BYTES>
+// BYTES at rsrc + off (BYTES a multiple of 16, or 8 or 4); 16-byte pieces
+// STRIDE bytes apart.
+template <int BYTES, int STRIDE = 16>
 __device__ __forceinline__ void load_raw_buf(Raw<BYTES>& r, __amdgpu_buffer_rsrc_t rs, uint32_t off) {
   if constexpr (BYTES % 16 == 0) {
 #pragma unroll
     for (int i = 0; i < BYTES / 16; ++i) {
-      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, kLoadNT);
+      const u32x4 x = __builtin_amdgcn_raw_buffer_load_b128(rs, off + STRIDE * i, 0, kLoadNT);
       r.w[4 * i + 0] = x[0]; r.w[4 * i + 1] = x[1]; r.w[4 * i + 2] = x[2]; r.w[4 * i + 3] = x[3];
     }
   } else if constexpr (BYTES == 8) {
@@ -267,7 +274,7 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, const TilePtr& t,
                                           Tile<D, KV, ST>& c, int lane16, int grp) {
   using C = Tile<D, KV, ST>;
   const __amdgpu_buffer_rsrc_t rk = tile_rsrc(t.k), rv = tile_rsrc(t.v);
-  if (FULL || lane16 < valid) load_raw_buf<C::KB>(c.k, rk, o.k);
+  if (FULL || lane16 < valid) load_raw_buf<C::KB, C::KSTRIDE>(c.k, rk, o.k);
   else zero_raw<C::KB>(c.k);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -447,12 +454,17 @@ template <int D>
 struct QRaw {
   u32x4 w[D / 32];
 };
-template <int D>
+// The query elements in the order of this lane's K elements (see Tile):
+// word w holds elements [32 w + 8 grp, +8) for 16-bit K, [grp*D/4 + 8 w, +8)
+// for int8 K.
+template <int D, class KV>
 __device__ __forceinline__ QRaw<D> load_q_raw(const DecodeArgs& a, int b, int hq, bool live, int grp) {
+  constexpr bool kInt8 = std::is_same<KV, I8>::value;
   QRaw<D> r;
-  const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + grp * (D / 4) * 2;
+  const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + (kInt8 ? grp * (D / 4) * 2 : grp * 16);
+  constexpr int STEP = kInt8 ? 16 : 64;
 #pragma unroll
-  for (int w = 0; w < D / 32; ++w) r.w[w] = live ? *(const u32x4*)(qp + 16 * w) : u32x4{0u, 0u, 0u, 0u};
+  for (int w = 0; w < D / 32; ++w) r.w[w] = live ? *(const u32x4*)(qp + STEP * w) : u32x4{0u, 0u, 0u, 0u};
   return r;
 }
 
@@ -603,7 +615,7 @@ void decode_main(const DecodeArgs a) {
   const int lane16 = lane & 15, grp = lane >> 4;
   using TileT = Tile<D, KV, ST>;
   LaneOff lo;
-  lo.k = lane16 * a.k_tok + (uint32_t)(grp * TileT::KB);
+  lo.k = lane16 * a.k_tok + (uint32_t)(grp * (TileT::kInt8 ? TileT::KB : 16));
 #pragma unroll
   for (int i = 0; i < 4; ++i) lo.v[i] = (4 * grp + i) * a.v_tok + (uint32_t)(lane16 * TileT::VB);
   lo.ks = 4 * grp * a.ks_tok;
@@ -660,7 +672,7 @@ void decode_main(const DecodeArgs a) {
       };
       // The loads that need only the item go out together: the query row
       // and the first tile's page id (the length is already in flight).
-      const QRaw<D> qraw = load_q_raw<D>(a, b, hq, live, grp);
+      const QRaw<D> qraw = load_q_raw<D, KV>(a, b, hq, live, grp);
       const int pg0 = page_id(0);
       const int t_full = min(t_hi, ntok / kTile);
       const int nfull = t_first < t_full ? (t_full - t_first + P - 1) / P : 0;
@@ -713,14 +725,17 @@ void decode_main(const DecodeArgs a) {
         qmul = prep_q<D, KV, QT>(a, qraw, qop, qop_lo);
         int k = 0;
         for (; k + 2 < nfull; k += 2) {
-          // Waves w and w^4 share a SIMD, where the older one wins issue
-          // ties and would finish well ahead: the one that is behind (by
-          // tile count, published in LDS) takes the higher priority.
-          __hip_atomic_store(&prog[wave], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);   // every lane, same value
-          if (k > uniform(__hip_atomic_load(&prog[wave ^ 4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)))
-            __builtin_amdgcn_s_setprio(0);
-          else
-            __builtin_amdgcn_s_setprio(1);
+          // With 8 waves, waves w and w^4 share a SIMD, where the older one
+          // wins issue ties and would finish well ahead: the one that is
+          // behind (by tile count, published in LDS) takes the higher
+          // priority.  (A 4-wave group has one wave per SIMD.)
+          if constexpr (NW == 8) {
+            __hip_atomic_store(&prog[wave], k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);   // every lane, same value
+            if (k > uniform(__hip_atomic_load(&prog[wave ^ 4], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)))
+              __builtin_amdgcn_s_setprio(0);
+            else
+              __builtin_amdgcn_s_setprio(1);
+          }
           const int pg1 = __builtin_amdgcn_readlane(pgv, 0), pg2 = __builtin_amdgcn_readlane(pgv, 1);
           load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first + (k + 1) * P, pg1), lo, 16, bufB, lane16, grp);
           pgv = page_pair(k + 3);
@@ -728,8 +743,10 @@ void decode_main(const DecodeArgs a) {
           load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first + (k + 2) * P, pg2), lo, 16, bufA, lane16, grp);
           compute_tile<D, KV, QT, ST, true>(bufB, qop, qop_lo, qmul, 0, ntok, grp, st);
         }
-        __builtin_amdgcn_s_setprio(0);
-        __hip_atomic_store(&prog[wave], 1 << 30, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if constexpr (NW == 8) {
+          __builtin_amdgcn_s_setprio(0);
+          __hip_atomic_store(&prog[wave], 1 << 30, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
         if (k + 1 < nfull) {
           load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first + (k + 1) * P, __builtin_amdgcn_readlane(pgv, 0)), lo,
                                          16, bufB, lane16, grp);

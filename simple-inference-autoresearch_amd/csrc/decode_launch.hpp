@@ -10,6 +10,13 @@ namespace sia {
 
 constexpr int kDecodeWaves = 8;   // waves per work-group: one per KV-head unit of a page
 
+// Waves per work-group of decode_main at head_dim D.  Up to D = 128 a group of
+// 8 waves runs two per SIMD with 256 registers each.  At D = 256 the
+// accumulators, the double-buffered tiles and the query operand need more
+// than 256 registers, so the group has 4 waves, one per SIMD, each with the
+// whole 512-entry register file (VGPRs plus AGPRs for the MFMA accumulators).
+constexpr int decode_waves(int D) { return D >= 256 ? 4 : kDecodeWaves; }
+
 struct DecodeLaunch {
   DecodeArgs a;
   int D;
@@ -27,7 +34,7 @@ inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
 
 template <int D, class KV, class QT, class ST>
 int launch_decode_typed(DecodeLaunch& L) {
-  constexpr int NW = kDecodeWaves;
+  constexpr int NW = decode_waves(D);
   // int8 K/V with fp32 scale rows: one 16-byte scale load per lane when the
   // rows allow it (decided on the host, compiled as two kernels)
   auto kmain = decode_main<D, KV, QT, ST, NW, false>;
