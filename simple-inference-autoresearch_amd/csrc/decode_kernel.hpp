@@ -204,8 +204,13 @@ struct Tile {
   // contiguous run (a 128-byte row is already one line per instruction).
   static constexpr int KB = (D / 4) * KV::bytes;
   static constexpr int KSTRIDE = std::is_same<KV, I8>::value ? 16 : 64;   // bytes between a lane's K pieces
-  static constexpr int VB = (D / 16) * KV::bytes;    // V bytes per lane per token: elems [lane16*D/16, +D/16)
+  static constexpr int VB = (D / 16) * KV::bytes;    // V bytes per lane per token (see kVSplit)
   static constexpr bool kInt8 = std::is_same<KV, I8>::value;
+  // V of one token: elements [lane16*D/16, +D/16), or, when a lane's share is
+  // more than 16 bytes (16-bit V at D = 256), 16-byte pieces 256 bytes apart,
+  // elements [128 p + 8 lane16, +8) for piece p, so that one load instruction
+  // reads whole 128-byte lines of the row.
+  static constexpr bool kVSplit = !kInt8 && VB > 16;
   Raw<KB> k;
   Raw<VB> v[4];                                      // tokens 4*grp + i
   float ks[4], vs[4];                                // int8 scales of tokens 4*grp + i
@@ -278,7 +283,7 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, const TilePtr& t,
   else zero_raw<C::KB>(c.k);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    if (FULL || 4 * grp + i < valid) load_raw_buf<C::VB>(c.v[i], rv, o.v[i]);
+    if (FULL || 4 * grp + i < valid) load_raw_buf<C::VB, C::kVSplit ? 256 : 16>(c.v[i], rv, o.v[i]);
     else zero_raw<C::VB>(c.v[i]);
   }
   if constexpr (C::kInt8) {
@@ -550,6 +555,15 @@ __device__ __forceinline__ float prep_q(const DecodeArgs& a, const QRaw<D>& raw,
   return mul;
 }
 
+// Head-dim index of accumulator element (e, i) of a lane in row group g: the
+// PV product's d-tile e holds, in output row 4 g + i, the element that lane
+// 4 g + i loaded as element e of its V share (see Tile).
+template <int D, class KV>
+__device__ __forceinline__ int out_d(int g, int i, int e) {
+  if constexpr (Tile<D, KV, F32>::kVSplit) return 128 * (e >> 3) + 32 * g + 8 * i + (e & 7);
+  else return g * (D / 4) + i * (D / 16) + e;
+}
+
 // Waves per SIMD each instantiation is compiled for (its VGPR budget).  A
 // work-group is NW = 8 waves, so below 4 waves per SIMD a CU holds one group.
 template <int D, class KV>
@@ -617,7 +631,7 @@ void decode_main(const DecodeArgs a) {
   LaneOff lo;
   lo.k = lane16 * a.k_tok + (uint32_t)(grp * (TileT::kInt8 ? TileT::KB : 16));
 #pragma unroll
-  for (int i = 0; i < 4; ++i) lo.v[i] = (4 * grp + i) * a.v_tok + (uint32_t)(lane16 * TileT::VB);
+  for (int i = 0; i < 4; ++i) lo.v[i] = (4 * grp + i) * a.v_tok + (uint32_t)(lane16 * (TileT::kVSplit ? 16 : TileT::VB));
   lo.ks = 4 * grp * a.ks_tok;
   lo.vs = 4 * grp * a.vs_tok;
   const int uin = wave / shape.P;        // unit slot of this wave inside an item
@@ -774,21 +788,21 @@ void decode_main(const DecodeArgs a) {
       if (live) {
         if (direct) {
           const float inv = unscale / (lsum == 0.f ? 1.f : lsum);
-          char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + grp * (D / 4) * 2;
+          char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int e = 0; e < E; e += 2) {
               const uint32_t w = pack2(QT{}, st.acc[e][i] * inv, st.acc[e + 1][i] * inv);
-              *(uint32_t*)(op + (i * E + e) * 2) = w;
+              *(uint32_t*)(op + out_d<D, KV>(grp, i, e) * 2) = w;
             }
         } else {
-          float* dst = a.ws_acc + (pslot + lane16) * D + grp * (D / 4);
+          float* dst = a.ws_acc + (pslot + lane16) * D;
 #pragma unroll
           for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int e = 0; e < E; e += 4)
-              *(f32x4*)(dst + i * E + e) = f32x4{st.acc[e][i] * unscale, st.acc[e + 1][i] * unscale,
+              *(f32x4*)(dst + out_d<D, KV>(grp, i, e)) = f32x4{st.acc[e][i] * unscale, st.acc[e + 1][i] * unscale,
                                                  st.acc[e + 2][i] * unscale, st.acc[e + 3][i] * unscale};
           if (grp == 0) {
             a.ws_ml[(pslot + lane16) * 2 + 0] = st.m;
@@ -799,11 +813,11 @@ void decode_main(const DecodeArgs a) {
     } else {
       // P waves per unit: merge their (m, l, acc) through LDS
       if (live) {
-        float* dst = l_acc + (wave * a.G16 + lane16) * D + grp * (D / 4);
+        float* dst = l_acc + (wave * a.G16 + lane16) * D;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-          for (int e = 0; e < E; ++e) dst[i * E + e] = st.acc[e][i] * unscale;
+          for (int e = 0; e < E; ++e) dst[out_d<D, KV>(grp, i, e)] = st.acc[e][i] * unscale;
       }
       if (lane16 < a.G16 && grp == 0) {
         l_m[wave * a.G16 + lane16] = live ? st.m : -INFINITY;
