@@ -923,40 +923,6 @@ __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
     for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
     return x;
   };
-  char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 4 * li * (int)sizeof(uint16_t);
-  constexpr int kFastPieces = 16;
-  if (nmax <= kFastPieces) {
-    // at most kFastPieces pieces per row (the common case): every load of
-    // the merge, (m, l) and this lane's slice of each piece, goes out in one
-    // round instead of three dependent ones
-    f32x4 x[kFastPieces];
-    float mv[kFastPieces], lv[kFastPieces];
-#pragma unroll
-    for (int t = 0; t < kFastPieces; ++t) {
-      const bool ok = work && t < nsplit;
-      const int64_t sl = ok ? slot(t) : 0;
-      x[t] = ok ? *(const f32x4*)(a.ws_acc + sl * D + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
-      const f32x2 ml = ok ? *(const f32x2*)(a.ws_ml + sl * 2) : f32x2{-INFINITY, 0.f};
-      mv[t] = ml[0];
-      lv[t] = ml[1];
-    }
-    float M = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < kFastPieces; ++t) M = fmaxf(M, mv[t]);
-    f32x4 A = {0.f, 0.f, 0.f, 0.f};
-    float L = 0.f;
-#pragma unroll
-    for (int t = 0; t < kFastPieces; ++t) {
-      const float w = mv[t] == -INFINITY ? 0.f : fast_exp2(mv[t] - M);
-      L += w * lv[t];
-      A += w * x[t];
-    }
-    if (!work) return;
-    const float inv = 1.0f / (L == 0.f ? 1.f : L);
-    *(uint32_t*)op = pack2(OT{}, A[0] * inv, A[1] * inv);
-    *(uint32_t*)(op + 4) = pack2(OT{}, A[2] * inv, A[3] * inv);
-    return;
-  }
   float M = -INFINITY;
   for (int s0 = 0; s0 < nmax; s0 += LPR) {
     const int s = s0 + li;
@@ -992,6 +958,7 @@ __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
   L = group_sum(L);
   if (!work) return;
   const float inv = 1.0f / (L == 0.f ? 1.f : L);
+  char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 4 * li * (int)sizeof(uint16_t);
   *(uint32_t*)op = pack2(OT{}, A[0] * inv, A[1] * inv);
   *(uint32_t*)(op + 4) = pack2(OT{}, A[2] * inv, A[3] * inv);
 }
