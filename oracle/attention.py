@@ -71,7 +71,12 @@ def quantize_kv_int8(x, src_dtype: str = "float32", scale_dtype: str = "float16"
     amax = np.max(np.abs(x32), axis=-1, keepdims=True).astype(np.float32)
     amax = np.maximum(amax, floor)
     scale = (amax / np.float32(127.0)).astype(np.float32)
-    xi = np.rint((x32 / scale).astype(np.float32))
+    # an all-zero fp16 row has scale 0 (1e-8 rounds to 0 in fp16): 0 / 0 is
+    # NaN, which torch's float -> int8 conversion turns into 0; stated
+    # explicitly here (numpy's NaN -> int8 cast is platform-defined)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        xi = np.rint((x32 / scale).astype(np.float32))
+    xi = np.where(np.isnan(xi), np.float32(0.0), xi)
     xi = np.clip(xi, -127, 127).astype(np.int8)
     scale = np.squeeze(scale, -1)
     if scale_dtype == "float16":
