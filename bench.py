@@ -484,7 +484,8 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8 K/V, bf16 q/out, fp32 softmax/accumulate",
+        "dtype": "int8",
+        "dtype_detail": "int8 K/V (QK on int8 MFMA, exact int32 dots), bf16 q/out, f16 PV MFMA, fp32 softmax/accumulate",
         "data": "synthetic (seeded N(0,1) K/V quantised per token per head; random page permutation)",
         "config": {
             "workload": {"cfg2": "config 2: paged fp16 decode B16 ctx U[256,4096]",
