@@ -197,7 +197,8 @@ int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_d
  * projection leaves them (strided slices are read in place); 16-byte aligned
  * rows.  Token t of sequence b has position p = start_pos_host + start_pos[b]
  * + t (start_pos as in sia_kv_write) and is rotated by table row p of
- * cos/sin ((Tc, D) or (Tc, D/2), first D/2 columns read): pairs as in
+ * cos/sin ((Tc, D) or (Tc, D/2), f16|bf16|f32, 16-byte aligned with row
+ * strides a multiple of 16 bytes, first D/2 columns read): pairs as in
  * sia_rope_qk (interleaved 0 or 1), the same fp32 arithmetic.  The rotated K
  * is rounded to k's dtype, then written like sia_kv_write writes k (cast, or
  * int8 with a per-token-per-head scale); v is written unrotated; q_out
