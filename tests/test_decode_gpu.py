@@ -367,3 +367,22 @@ def test_argument_errors(gpu_pkg):
     bt = torch.zeros(2, 2, dtype=torch.int32, device=DEV)
     with pytest.raises(AssertionError):
         gpu_pkg.paged_attention_flash_decode(q, pool, pool, bt, kl, 32)
+
+
+@pytest.mark.parametrize("Hkv", [1, 2, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("tps", [0, 1, 3])
+def test_head_dim_256_unit_shapes_and_splits(gpu_pkg, Hkv, dtype, tps):
+    """head_dim 256 runs 4-wave groups whose V shares and outputs use their own element order:
+    every unit shape (1, 2 or 4 waves per KV head, or several heads per group) and forced
+    split-K pieces (partials written in that order, then merged) against the oracle."""
+    announce(f"D=256 decode Hkv={Hkv} {dtype} tiles_per_split={tps}")
+    B, G, S, D = 3, 4, 150, 256
+    q, k, v, _, _ = contiguous_case(B, G * Hkv, Hkv, S, D, dtype, dtype, seed=256 + Hkv)
+    lens = [150, 17, 96]
+    kl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    with gpu_pkg.decode_options(tiles_per_split=tps):
+        out = gpu_pkg.attention_flash_decode(q, k, v, kl)
+    torch.cuda.synchronize()
+    ref = O.gqa_decode(f64(q), f64(k), f64(v), lens)
+    assert_close(out, ref, 2e-3, f"D=256 Hkv={Hkv} {dtype} tps={tps}")
