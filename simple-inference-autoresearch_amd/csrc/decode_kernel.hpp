@@ -197,13 +197,14 @@ __device__ __forceinline__ int sk_group(int x, int W, int G) {
 // One 16-token tile's operands as held by one lane.
 template <int D, class KV, class ST>
 struct Tile {
-  // K bytes per lane, token lane16.  16-bit K: 16 bytes per k-step j at
-  // elements [32 j + 8 grp, +8), the MFMA operand's own order, so the 4 lanes
-  // of a row read 64 contiguous bytes per load instruction (16 cache lines
-  // per instruction instead of 64).  int8 K: elements [grp*D/4, +D/4), one
-  // contiguous run (a 128-byte row is already one line per instruction).
+  // K bytes per lane, token lane16: 16 bytes per MFMA k-step j, at bytes
+  // [64 j + 16 grp, +16) of the row (elements [32 j + 8 grp, +8) for 16-bit
+  // K, [64 j + 16 grp, +16) for int8), the operand's own order, so the 4
+  // lanes of a row read 64 contiguous bytes per load instruction.  (A lane
+  // owning a contiguous quarter of the row instead made every 16-bit load
+  // instruction touch 64 cache lines at 16 bytes each.)
   static constexpr int KB = (D / 4) * KV::bytes;
-  static constexpr int KSTRIDE = std::is_same<KV, I8>::value ? 16 : 64;   // bytes between a lane's K pieces
+  static constexpr int KSTRIDE = 64;                                      // bytes between a lane's K pieces
   static constexpr int VB = (D / 16) * KV::bytes;    // V bytes per lane per token (see kVSplit)
   static constexpr bool kInt8 = std::is_same<KV, I8>::value;
   // V of one token: elements [lane16*D/16, +D/16), or, when a lane's share is
@@ -460,16 +461,19 @@ struct QRaw {
   u32x4 w[D / 32];
 };
 // The query elements in the order of this lane's K elements (see Tile):
-// word w holds elements [32 w + 8 grp, +8) for 16-bit K, [grp*D/4 + 8 w, +8)
-// for int8 K.
+// word w holds elements [32 w + 8 grp, +8) for 16-bit K, and for int8 K
+// words 2j and 2j+1 hold elements [64 j + 16 grp, +16) (k-step j).
 template <int D, class KV>
 __device__ __forceinline__ QRaw<D> load_q_raw(const DecodeArgs& a, int b, int hq, bool live, int grp) {
   constexpr bool kInt8 = std::is_same<KV, I8>::value;
   QRaw<D> r;
-  const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + (kInt8 ? grp * (D / 4) * 2 : grp * 16);
-  constexpr int STEP = kInt8 ? 16 : 64;
+  const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + (kInt8 ? grp * 32 : grp * 16);
 #pragma unroll
-  for (int w = 0; w < D / 32; ++w) r.w[w] = live ? *(const u32x4*)(qp + STEP * w) : u32x4{0u, 0u, 0u, 0u};
+  for (int w = 0; w < D / 32; ++w) {
+    // int8: k-step w/2 covers elements [64 (w/2) + 16 grp, +16) in two words
+    const int off = kInt8 ? 128 * (w >> 1) + 16 * (w & 1) : 64 * w;
+    r.w[w] = live ? *(const u32x4*)(qp + off) : u32x4{0u, 0u, 0u, 0u};
+  }
   return r;
 }
 
@@ -629,7 +633,7 @@ void decode_main(const DecodeArgs a) {
   const int lane16 = lane & 15, grp = lane >> 4;
   using TileT = Tile<D, KV, ST>;
   LaneOff lo;
-  lo.k = lane16 * a.k_tok + (uint32_t)(grp * (TileT::kInt8 ? TileT::KB : 16));
+  lo.k = lane16 * a.k_tok + (uint32_t)(grp * 16);
 #pragma unroll
   for (int i = 0; i < 4; ++i) lo.v[i] = (4 * grp + i) * a.v_tok + (uint32_t)(lane16 * (TileT::kVSplit ? 16 : TileT::VB));
   lo.ks = 4 * grp * a.ks_tok;
