@@ -55,14 +55,3 @@ def eager_paged_int8_decode(q, k_pool, v_pool, ks_pool, vs_pool, block_table, kv
         outs.append(eager_gqa(q[b:b + 1], k[None], v[None], causal=False))
     return torch.cat(outs, 0)
 
-
-def eager_paged_decode(q, k_pool, v_pool, block_table, kv_len, page: int, batch_rows=None) -> torch.Tensor:
-    """Reference CPU path for paged fp16/bf16 decode (gather, then eager GQA in fp32)."""
-    rows = range(q.shape[0]) if batch_rows is None else batch_rows
-    outs = []
-    for b in rows:
-        n = int(kv_len[b])
-        k = gather_pages(k_pool, block_table, b, n, page).float()
-        v = gather_pages(v_pool, block_table, b, n, page).float()
-        outs.append(eager_gqa(q[b:b + 1].float(), k[None], v[None], causal=False))
-    return torch.cat(outs, 0)

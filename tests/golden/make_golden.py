@@ -15,6 +15,8 @@ decode_gqa.json      single-query GQA decode, per-sequence kv_len (incl. 1 and S
 prefill_causal.json  causal attention with Tq < Tk (bottom-right offset)
 prefill_masked.json  causal with Tq > Tk: leading rows fully masked -> zeros
 paged_decode.json    paged pool with a permuted block table, ragged lengths
+paged_int8_decode.json  paged int8 pools with distinct per-token-per-head K and V
+                     scale pools, GQA, a permuted block table, ragged lengths
 quant_int8.json      per-vector int8 quantisation known answers
 splitk_merge.json    (m, l, acc) partials over key ranges and their merge
 """
@@ -131,6 +133,50 @@ def case_paged():
                 page_size=page, sm_scale=scale, nblk=nblk, out=out)
 
 
+def case_paged_int8():
+    """Paged INT8-KV GQA decode by hand: token t of sequence b is slot t % page of
+    page block_table[b][t // page]; its key is k_i8 * k_scale and its value
+    v_i8 * v_scale, both scales read at (page, kv head, slot).  K and V scales
+    are drawn from different ranges, so swapping them changes the output."""
+    r = LCG(53)
+    B, Hq, Hkv, D, page = 2, 4, 2, 3, 2
+    NB = 7
+    kv_len = [5, 4]
+    block_table = [[6, 1, 3], [0, 4, 2]]          # row 1's third entry is unused padding
+
+    def i8_tensor(shape):
+        if len(shape) == 1:
+            return [int(round(r.next() * 127.0)) for _ in range(shape[0])]
+        return [i8_tensor(shape[1:]) for _ in range(shape[0])]
+
+    def f32_tensor(shape, lo, hi):
+        if len(shape) == 1:
+            return [f32(lo + (hi - lo) * (r.next() + 1.0) / 2.0) for _ in range(shape[0])]
+        return [f32_tensor(shape[1:], lo, hi) for _ in range(shape[0])]
+
+    k_pool = i8_tensor([NB, Hkv, page, D])
+    v_pool = i8_tensor([NB, Hkv, page, D])
+    k_scale = f32_tensor([NB, Hkv, page], 0.002, 0.02)
+    v_scale = f32_tensor([NB, Hkv, page], 0.05, 0.5)
+    q = r.tensor([B, Hq, 1, D], 3.0)
+    scale = 0.6
+    G = Hq // Hkv
+    out = []
+    for b in range(B):
+        rows = []
+        for hq in range(Hq):
+            h = hq // G
+            keys, vals = [], []
+            for t in range(kv_len[b]):
+                pg, slot = block_table[b][t // page], t % page
+                keys.append([k_pool[pg][h][slot][d] * k_scale[pg][h][slot] for d in range(D)])
+                vals.append([v_pool[pg][h][slot][d] * v_scale[pg][h][slot] for d in range(D)])
+            rows.append(softmax_rows(q[b][hq][0], keys, vals, scale))
+        out.append([rows])
+    return dict(q=q, k_pool=k_pool, v_pool=v_pool, k_scale=k_scale, v_scale=v_scale,
+                block_table=block_table, kv_len=kv_len, page_size=page, sm_scale=scale, out=out)
+
+
 def quant_vec(x, scale_dtype):
     """model/kv_cache.py:58-67 by hand, float32 emulated with struct."""
     xs = [f32(e) for e in x]
@@ -198,6 +244,7 @@ def main():
         "prefill_causal.json": case_prefill(17, 1, 4, 2, 3, 6, 3, 0.8),
         "prefill_masked.json": case_prefill(23, 1, 2, 1, 4, 2, 3, 1.1),
         "paged_decode.json": case_paged(),
+        "paged_int8_decode.json": case_paged_int8(),
         "quant_int8.json": case_quant(),
         "splitk_merge.json": case_splitk(),
     }
