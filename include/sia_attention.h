@@ -83,8 +83,12 @@ int sia_decode_workspace_size(int64_t batch, int64_t num_q_heads, int64_t num_kv
 
 /* Replaces attention_flash_decode (kernels/flash_decode_kernel.py:119-160).
  * Every decode entry point takes head_dim 16, 32, 64, 128 or 256.
- * q (B,Hq,1,D) f16|bf16; k,v (B,Hkv,S,D) same dtype as q (views into the cache);
- * kv_len int32 (1,)|()|(B,) on device; out (B,1,Hq,D) dtype of q. */
+ * q (B,Hq,1,D) f16|bf16|f32; k,v (B,Hkv,S,D) f16|bf16|f32 (views into the
+ * cache); kv_len int32 (1,)|()|(B,) on device; out (B,1,Hq,D) dtype of q,
+ * 16-byte aligned rows.  16-bit q and K/V run on the MFMA kernels; a float32
+ * q or K/V runs every product in fp32 on the vector ALUs, as the reference's
+ * decode kernel does (kernels/flash_decode_kernel.py:85-114).  Every decode
+ * entry point accepts an f32 q the same way. */
 int sia_attention_flash_decode(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v,
                                const sia_tensor* kv_len, float sm_scale, const sia_tensor* out,
                                void* workspace, size_t workspace_bytes,
@@ -134,7 +138,7 @@ int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_poo
                                     const sia_decode_options* opts, void* stream);
 
 /* Replaces attention_flash_triton (kernels/attention_kernel.py:235-305).
- * q (B,Hq,Tq,D), k,v (B,Hkv,Tk,D): f16|bf16 views, head_dim contiguous,
+ * q (B,Hq,Tq,D), k,v (B,Hkv,Tk,D): f16|bf16|f32 views (one dtype), head_dim contiguous,
  * 16-byte aligned rows; out (B,Hq,Tq,D) view in q's dtype -- a transposed
  * view of a (B,Tq,Hq,D) buffer gives the reference's out_token_major layout.
  * causal != 0 applies the bottom-right mask: row i sees keys <= (Tk-Tq)+i;
@@ -142,7 +146,8 @@ int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_poo
  * (the reference's assert set, kernels/attention_kernel.py:273).
  * workspace: device memory of at least sia_prefill_workspace_size bytes
  * (256-byte aligned); it holds V converted to f16 in the kernel's block
- * layout and is free again when the stream passes the call. */
+ * layout and is free again when the stream passes the call.  f32 inputs run
+ * in fp32 on the vector ALUs and need no workspace (NULL, 0 is accepted). */
 int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
                             float sm_scale, const sia_tensor* out, void* workspace, size_t workspace_bytes,
                             void* stream);

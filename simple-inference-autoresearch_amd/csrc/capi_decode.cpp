@@ -2,6 +2,7 @@
 #include <math.h>
 #include <string.h>
 
+#include "attn_f32.hpp"
 #include "decode_launch.hpp"
 #include "host_util.hpp"
 
@@ -65,8 +66,8 @@ int prepare_common(const sia_tensor* q, const sia_tensor* kv_len, const sia_tens
   if ((rc = check_tensor(out, "out", 4))) return rc;
   if (kv_len == nullptr || kv_len->data == nullptr)
     return fail(SIA_ERR_INVALID_ARGUMENT, "kv_len is missing");
-  if (q->dtype != SIA_F16 && q->dtype != SIA_BF16)
-    return fail(SIA_ERR_UNSUPPORTED, "q dtype %s: expected float16 or bfloat16", dtype_name(q->dtype));
+  if (q->dtype != SIA_F16 && q->dtype != SIA_BF16 && q->dtype != SIA_F32)
+    return fail(SIA_ERR_UNSUPPORTED, "q dtype %s: expected float16, bfloat16 or float32", dtype_name(q->dtype));
   if (q->shape[2] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "decode kernel expects a single query position");
   if ((rc = geometry(q->shape[0], q->shape[1], Hkv, q->shape[3], g))) return rc;
   if (g.D != 16 && g.D != 32 && g.D != 64 && g.D != 128 && g.D != 256)
@@ -214,6 +215,73 @@ int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decod
   return SIA_OK;
 }
 
+// Float32 q or K/V: the vector-ALU path (attn_f32.hpp).  Same checked
+// arguments as the MFMA path; the key range is split on the host from the
+// cache capacity so that the partials fit the caller's workspace.
+int dispatch_f32(const DecodeLaunch& D, const Geometry& g, int kv_dtype, const sia_tensor* out) {
+  const DecodeArgs& d = D.a;
+  if (!aligned16(out->data) || bstride(out, 0) % 16 || bstride(out, 2) % 16)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "out rows must be 16-byte aligned");
+  F32Launch L;
+  memset(&L, 0, sizeof(L));
+  F32Args& a = L.a;
+  a.q = d.q; a.q_sb = d.q_sb; a.q_sh = d.q_sh; a.q_sm = 0;
+  a.out = d.out; a.o_sb = d.o_sb; a.o_sh = d.o_sh; a.o_sm = 0;
+  a.k = d.k; a.k_s0 = d.k_s0; a.k_sh = d.k_sh; a.k_sn = d.k_sn;
+  a.v = d.v; a.v_s0 = d.v_s0; a.v_sh = d.v_sh; a.v_sn = d.v_sn;
+  a.ks = d.ks; a.ks_s0 = d.ks_s0; a.ks_sh = d.ks_sh; a.ks_sn = d.ks_sn;
+  a.vs = d.vs; a.vs_s0 = d.vs_s0; a.vs_sh = d.vs_sh; a.vs_sn = d.vs_sn;
+  a.bt = d.bt; a.bt_sb = d.bt_sb; a.bt_sl = d.bt_sl;
+  a.num_pages = d.num_pages;
+  a.page_size = kTile << d.lg_tiles_per_page;
+  a.kv_len = d.kv_len; a.kv_per_seq = d.kv_per_seq;
+  a.cap = d.cap_tokens;
+  a.B = g.B; a.Hq = g.Hq; a.Hkv = g.Hkv; a.G = g.G; a.Tq = 1; a.Tk = d.cap_tokens; a.causal = 0;
+  a.ncol = g.G;
+  a.nchunk = (g.G + kF32Cols - 1) / kF32Cols;
+  a.qk_scale = d.qk_scale;
+  // split: enough items for four per CU, pieces of >= 256 keys, within the workspace
+  const int64_t rows = (int64_t)g.B * g.Hq;
+  const int64_t base = (int64_t)g.B * g.Hkv * a.nchunk;
+  const int64_t cap = a.cap > 0 ? a.cap : 1;
+  int64_t tps;
+  if (d.tps_force > 0) {
+    tps = (int64_t)d.tps_force * kTile;
+  } else {
+    const int cus = device_info().cus > 0 ? device_info().cus : 256;
+    int64_t want = (4LL * cus + base - 1) / base;
+    want = want < 1 ? 1 : want;
+    const int64_t most = (cap + 255) / 256;
+    if (want > most) want = most;
+    tps = (cap + want - 1) / want;
+  }
+  tps = (tps + kTile - 1) / kTile * kTile;
+  int64_t nsplit = (cap + tps - 1) / tps;
+  if (nsplit > 1) {
+    const size_t room = D.ws_bytes;
+    const int64_t fit = (int64_t)(room / f32_partial_bytes(rows, 1, g.D));
+    if (fit < 2) {
+      nsplit = 1;
+    } else if (nsplit > fit) {
+      tps = ((cap + fit - 1) / fit + kTile - 1) / kTile * kTile;
+      nsplit = (cap + tps - 1) / tps;
+    }
+  }
+  if (nsplit == 1) tps = cap;
+  if (tps > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "cache length too large");
+  a.nsplit = (int)nsplit;
+  a.tps = (int)tps;
+  a.part = (float*)D.ws;
+  L.D = g.D;
+  L.q_dtype = D.q_dtype;
+  L.kv_dtype = kv_dtype;
+  L.scale_dtype = D.scale_dtype;
+  L.stream = D.stream;
+  L.begin_event = D.begin_event;
+  L.end_event = D.end_event;
+  return launch_attn_f32(L);
+}
+
 int dispatch(DecodeLaunch& L, int kv_dtype) {
   switch (kv_dtype) {
     case SIA_F16: return launch_decode_f16(L);
@@ -237,12 +305,16 @@ int decode_any(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, co
   if (want_int8) {
     if (k->dtype != SIA_I8) return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be int8 for the int8 entry points");
     if ((rc = prepare_scales(ks, vs, k, bt != nullptr, L))) return rc;
-  } else if (k->dtype != SIA_F16 && k->dtype != SIA_BF16) {
-    return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be float16 or bfloat16 (use the int8 entry points for int8)");
+  } else if (k->dtype != SIA_F16 && k->dtype != SIA_BF16 && k->dtype != SIA_F32) {
+    return fail(SIA_ERR_INVALID_ARGUMENT,
+                "k/v must be float16, bfloat16 or float32 (use the int8 entry points for int8)");
   }
   if (bt != nullptr && (rc = prepare_table(bt, g, page_size, L))) return rc;
   if ((rc = prepare_workspace(ws, ws_bytes, g, opts, L))) return rc;
   L.stream = (hipStream_t)stream;
+  L.ws = ws;
+  L.ws_bytes = ws_bytes;
+  if (q->dtype == SIA_F32 || k->dtype == SIA_F32) return dispatch_f32(L, g, k->dtype, out);
   return dispatch(L, k->dtype);
 }
 

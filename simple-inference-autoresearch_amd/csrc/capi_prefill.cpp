@@ -2,6 +2,7 @@
 #include <math.h>
 #include <string.h>
 
+#include "attn_f32.hpp"
 #include "host_util.hpp"
 #include "prefill_launch.hpp"
 
@@ -28,6 +29,40 @@ int64_t image_bytes(int64_t B, int64_t Hkv, int64_t Tk, int64_t D) {
   return B * Hkv * nkb * kPfBN * DV * 2;
 }
 
+// Float32 q/k/v: the vector-ALU path (attn_f32.hpp), one work item per
+// (sequence, KV head, chunk of query rows x heads), no workspace.
+int prefill_f32(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal, float sm_scale,
+                const sia_tensor* out, void* stream) {
+  const int64_t B = q->shape[0], Hq = q->shape[1], Tq = q->shape[2], D = q->shape[3];
+  const int64_t Hkv = k->shape[1], Tk = k->shape[2];
+  const int64_t G = Hq / Hkv;
+  if (Tq * G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "too many query rows");
+  const DeviceInfo& dev = device_info();
+  if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
+  if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
+  if (Tq == 0) return SIA_OK;
+  F32Launch L;
+  memset(&L, 0, sizeof(L));
+  F32Args& a = L.a;
+  a.q = (const char*)q->data; a.q_sb = bstride(q, 0); a.q_sh = bstride(q, 1); a.q_sm = bstride(q, 2);
+  a.out = (char*)out->data; a.o_sb = bstride(out, 0); a.o_sh = bstride(out, 1); a.o_sm = bstride(out, 2);
+  a.k = (const char*)k->data; a.k_s0 = bstride(k, 0); a.k_sh = bstride(k, 1); a.k_sn = bstride(k, 2);
+  a.v = (const char*)v->data; a.v_s0 = bstride(v, 0); a.v_sh = bstride(v, 1); a.v_sn = bstride(v, 2);
+  a.cap = (int)Tk;
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)G; a.Tq = (int)Tq; a.Tk = (int)Tk;
+  a.causal = causal != 0;
+  a.ncol = (int)(Tq * G);
+  a.nchunk = (int)((Tq * G + kF32Cols - 1) / kF32Cols);
+  a.nsplit = 1;
+  a.tps = Tk > 0 ? (int)Tk : 1;
+  a.qk_scale = sm_scale * 1.4426950408889634f;
+  L.D = (int)D;
+  L.q_dtype = SIA_F32;
+  L.kv_dtype = SIA_F32;
+  L.stream = (hipStream_t)stream;
+  return launch_attn_f32(L);
+}
+
 }  // namespace
 
 extern "C" int sia_prefill_workspace_size(int64_t batch, int64_t kv_heads, int64_t kv_len, int64_t head_dim,
@@ -46,8 +81,8 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
                                        size_t workspace_bytes, void* stream) {
   int rc;
   if ((rc = check4(q, "q")) || (rc = check4(k, "k")) || (rc = check4(v, "v")) || (rc = check4(out, "out"))) return rc;
-  if (q->dtype != SIA_F16 && q->dtype != SIA_BF16)
-    return fail(SIA_ERR_UNSUPPORTED, "q dtype %s: expected float16 or bfloat16", dtype_name(q->dtype));
+  if (q->dtype != SIA_F16 && q->dtype != SIA_BF16 && q->dtype != SIA_F32)
+    return fail(SIA_ERR_UNSUPPORTED, "q dtype %s: expected float16, bfloat16 or float32", dtype_name(q->dtype));
   if (k->dtype != q->dtype || v->dtype != q->dtype || out->dtype != q->dtype)
     return fail(SIA_ERR_INVALID_ARGUMENT, "q, k, v and out must share one dtype");
   const int64_t B = q->shape[0], Hq = q->shape[1], Tq = q->shape[2], D = q->shape[3];
@@ -68,6 +103,7 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
     return fail(SIA_ERR_UNSUPPORTED, "k token stride %lld bytes: expected [%lld, 2^31/64)", (long long)k_sn,
                 (long long)(2 * D));
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return fail(SIA_ERR_INVALID_ARGUMENT, "sm_scale must be positive");
+  if (q->dtype == SIA_F32) return prefill_f32(q, k, v, causal, sm_scale, out, stream);
   const int64_t need = image_bytes(B, Hkv, Tk, D);
   if (need > 0 && (workspace == nullptr || (uintptr_t)workspace % 256 || workspace_bytes < (size_t)need))
     return fail(SIA_ERR_WORKSPACE, "prefill workspace missing, misaligned or smaller than %lld bytes",

@@ -20,11 +20,13 @@ constexpr int decode_waves(int D) { return D >= 256 ? 4 : kDecodeWaves; }
 struct DecodeLaunch {
   DecodeArgs a;
   int D;
-  int q_dtype;       // SIA_F16 / SIA_BF16 (also the output dtype)
+  int q_dtype;       // SIA_F16 / SIA_BF16 / SIA_F32 (also the output dtype)
   int scale_dtype;   // SIA_F32 / SIA_F16 (int8 only)
   hipStream_t stream;
   hipEvent_t begin_event;   // optional, recorded around the main kernel
   hipEvent_t end_event;
+  void* ws;                 // the caller's workspace (the fp32 path lays it out itself)
+  size_t ws_bytes;
 };
 
 inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {

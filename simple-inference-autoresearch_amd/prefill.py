@@ -78,7 +78,8 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
         else:
             out = torch.empty((B, Hq, Tq, D), dtype=q.dtype, device=q.device)
             out_view = out
-        nbytes = prefill_workspace_size(B, Hkv, Tk, D)
+        # float32 calls run on the vector-ALU kernel, which needs no V images
+        nbytes = 0 if q.dtype == torch.float32 else prefill_workspace_size(B, Hkv, Tk, D)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
         dq, dk, dv, do = (_lib.desc(t) for t in (q, k, v, out_view))
         rc = h.sia_attention_flash_fwd(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv),
