@@ -1,13 +1,26 @@
-"""ctypes binding of ``libsia_attention.so`` (the gfx950 C ABI in include/sia_attention.h).
+"""Loading of ``libsia_attention.so`` (the gfx950 C ABI in include/sia_attention.h).
 
-The library is loaded lazily, after ``import torch`` so that it shares torch's
-HIP runtime (both resolve ``libamdhip64.so.7``).  There is no fallback: when the
-library is missing every kernel call raises ``LibraryMissing``.
+Two bindings of the same library:
+
+* ``ops()`` -- the thin torch extension ``_sia_ops.so`` (built from
+  ``torch_ext/sia_ops.cpp``), which every kernel call of this package goes
+  through: it checks devices, describes the tensors, takes outputs and
+  workspace from torch's caching allocator and calls the C ABI on torch's
+  current stream, in C++.
+* ``load_library()`` -- a ctypes handle on the C ABI itself, for the ABI
+  version check, status strings and symbol checks, and as the template of an
+  FFI binding from another host language.
+
+Both are loaded lazily, after ``import torch`` so that the library shares
+torch's HIP runtime (both resolve ``libamdhip64.so.7``).  There is no
+fallback: when either is missing every kernel call raises ``LibraryMissing``.
 """
 
 from __future__ import annotations
 
 import ctypes
+import importlib.machinery
+import importlib.util
 import os
 import threading
 
@@ -15,6 +28,8 @@ import torch
 
 LIB_NAME = "libsia_attention.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+EXT_NAME = "_sia_ops"
+EXT_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), EXT_NAME + ".so")
 
 SIA_MAX_DIMS = 5
 SIA_F16, SIA_BF16, SIA_F32, SIA_I8, SIA_I32, SIA_I64, SIA_U8 = range(7)
@@ -98,6 +113,8 @@ _STRING_RESULT = {"sia_status_string", "sia_last_error_message"}
 
 _lock = threading.Lock()
 _lib = None
+_ops = None
+_gpu_checked = False
 
 
 def library_path() -> str:
@@ -143,6 +160,42 @@ def require_library():
     return h
 
 
+def ops():
+    """The torch extension module (loaded once, after the library); raises LibraryMissing."""
+    global _ops
+    if _ops is not None:
+        return _ops
+    load_library()
+    with _lock:
+        if _ops is not None:
+            return _ops
+        if not os.path.exists(EXT_PATH):
+            raise LibraryMissing(
+                f"{EXT_NAME}.so is not built (expected at {EXT_PATH}); run __graft_entry__.build() "
+                "or python simple-inference-autoresearch_amd/csrc/build.py")
+        try:
+            loader = importlib.machinery.ExtensionFileLoader(EXT_NAME, EXT_PATH)
+            spec = importlib.util.spec_from_file_location(EXT_NAME, EXT_PATH, loader=loader)
+            mod = importlib.util.module_from_spec(spec)
+            loader.exec_module(mod)
+        except ImportError as exc:  # pragma: no cover - depends on the host
+            raise LibraryMissing(f"cannot load {EXT_PATH}: {exc}") from exc
+        if mod.abi_version() != 1:
+            raise LibraryMissing("_sia_ops.so was built against another ABI version; rebuild it")
+        mod.set_error_class(SiaError)
+        _ops = mod
+        return _ops
+
+
+def gpu_ops():
+    """``ops()`` once a GPU has been seen (checked on the first call only)."""
+    global _gpu_checked
+    if not _gpu_checked:
+        require_library()
+        _gpu_checked = True
+    return ops()
+
+
 def dtype_code(dt: torch.dtype) -> int:
     try:
         return _DTYPE_CODES[dt]
@@ -150,8 +203,15 @@ def dtype_code(dt: torch.dtype) -> int:
         raise ValueError(f"dtype {dt} is not supported by the attention kernels") from None
 
 
-def desc(t: torch.Tensor) -> SiaTensor:
-    """Describe a device tensor (pointer, dtype, shape, element strides)."""
+def desc(t: torch.Tensor, device: torch.device | None = None) -> SiaTensor:
+    """Describe a device tensor (pointer, dtype, shape, element strides) for a ctypes call.
+
+    The tensor must be a GPU tensor, on ``device`` when given: a host tensor
+    would hand a host address to the kernels.
+    """
+    if not t.is_cuda or (device is not None and t.device != device):
+        raise ValueError(f"tensor on {t.device}: the attention kernels need every tensor on "
+                         f"{device if device is not None else 'the GPU'}")
     if t.dim() > SIA_MAX_DIMS:
         raise ValueError(f"tensor with {t.dim()} dims; at most {SIA_MAX_DIMS} supported")
     d = SiaTensor()

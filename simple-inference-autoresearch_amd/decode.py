@@ -27,7 +27,6 @@ Differences that only widen the reference's contract:
 from __future__ import annotations
 
 import contextlib
-import ctypes
 import threading
 
 import torch
@@ -68,10 +67,7 @@ def decode_workspace_size(batch: int, num_q_heads: int, num_kv_heads: int, head_
     key = (batch, num_q_heads, num_kv_heads, head_dim, torch.cuda.current_device())
     n = _ws_cache.get(key)
     if n is None:
-        h = _lib.require_library()
-        out = ctypes.c_size_t(0)
-        _lib.check(h.sia_decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim, ctypes.byref(out)))
-        n = _ws_cache[key] = int(out.value)
+        n = _ws_cache[key] = int(_lib.gpu_ops().decode_workspace_size(batch, num_q_heads, num_kv_heads, head_dim))
     return n
 
 
@@ -79,44 +75,25 @@ def _kv_len_tensor(kv_len, device: torch.device) -> torch.Tensor:
     if isinstance(kv_len, torch.Tensor):
         if kv_len.dtype != torch.int32:
             raise ValueError("kv_len must be an int32 tensor")
-        if kv_len.device != device:
-            raise ValueError("kv_len must live on the same device as q")
         return kv_len
     # a device fill (no host-to-device copy), so the call can still be captured in a graph
     return torch.full((1,), int(kv_len), dtype=torch.int32, device=device)
 
 
-def _options():
+# decode kinds of the extension's decode op (one per C entry point)
+CONTIG, CONTIG_INT8, GQA_INT8, PAGED, PAGED_INT8 = range(5)
+
+
+def _run(kind: int, q: torch.Tensor, k, v, k_scale, v_scale, block_table, kv_len, page_size: int,
+         sm_scale: float) -> torch.Tensor:
+    """One decode call through the torch extension (device checks, output and workspace in C++)."""
+    ops = _lib.gpu_ops()
     tps = getattr(_tls, "tiles_per_split", 0)
     ev = getattr(_tls, "main_events", None)
-    if not tps and ev is None:
-        return None
-    o = _lib.DecodeOptions()
-    o.tiles_per_split = tps
+    b = e = 0
     if ev is not None:
-        o.main_begin_event = ev[0].cuda_event
-        o.main_end_event = ev[1].cuda_event
-    return ctypes.byref(o)
-
-
-def _run(fn_name: str, q: torch.Tensor, tensors, scalars, Hkv: int, sm_scale: float) -> torch.Tensor:
-    h = _lib.require_library()
-    if not q.is_cuda:
-        raise ValueError("decode attention runs on the GPU: q must be a CUDA (HIP) tensor")
-    B, Hq, Tq, D = q.shape
-    with torch.cuda.device(q.device):
-        out = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
-        ws_bytes = decode_workspace_size(B, Hq, Hkv, D)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-        descs = [_lib.desc(t) for t in tensors]
-        args = [ctypes.byref(d) for d in descs]
-        out_desc = _lib.desc(out)
-        rc = getattr(h, fn_name)(
-            *args, *scalars, ctypes.c_float(sm_scale), ctypes.byref(out_desc),
-            ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(ws_bytes), _options(),
-            ctypes.c_void_p(_lib.stream_handle(q.device)))
-        _lib.check(rc)
-    return out
+        b, e = ev[0].cuda_event, ev[1].cuda_event
+    return ops.decode(kind, q, k, v, k_scale, v_scale, block_table, kv_len, page_size, sm_scale, tps, b, e)
 
 
 def _common(q: torch.Tensor, k: torch.Tensor, sm_scale):
@@ -136,7 +113,7 @@ def attention_flash_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kv
     """
     scale = _common(q, k, sm_scale)
     kl = _kv_len_tensor(kv_len, q.device)
-    return _run("sia_attention_flash_decode", q, [q, k, v, kl], [], k.shape[1], scale)
+    return _run(CONTIG, q, k, v, None, None, None, kl, 0, scale)
 
 
 def attention_flash_decode_int8(q: torch.Tensor, k_int8: torch.Tensor, v_int8: torch.Tensor,
@@ -148,8 +125,7 @@ def attention_flash_decode_int8(q: torch.Tensor, k_int8: torch.Tensor, v_int8: t
     """
     scale = _common(q, k_int8, sm_scale)
     kl = _kv_len_tensor(kv_len, q.device)
-    return _run("sia_attention_flash_decode_int8", q, [q, k_int8, v_int8, k_scale, v_scale, kl], [],
-                k_int8.shape[1], scale)
+    return _run(CONTIG_INT8, q, k_int8, v_int8, k_scale, v_scale, None, kl, 0, scale)
 
 
 def gqa_int8_flash_decode(q, k_int8, v_int8, k_scale, v_scale, kv_len, sm_scale=None):
@@ -160,8 +136,7 @@ def gqa_int8_flash_decode(q, k_int8, v_int8, k_scale, v_scale, kv_len, sm_scale=
     """
     scale = _common(q, k_int8, sm_scale)
     kl = _kv_len_tensor(kv_len, q.device)
-    return _run("sia_gqa_int8_flash_decode", q, [q, k_int8, v_int8, k_scale, v_scale, kl], [],
-                k_int8.shape[1], scale)
+    return _run(GQA_INT8, q, k_int8, v_int8, k_scale, v_scale, None, kl, 0, scale)
 
 
 def paged_attention_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
@@ -179,8 +154,7 @@ def paged_attention_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: 
     _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
     scale = (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
     kl = _kv_len_tensor(kv_len, q.device)
-    return _run("sia_paged_attention_flash_decode", q, [q, k_pool, v_pool, block_table, kl],
-                [ctypes.c_int32(page_size)], Hkv, scale)
+    return _run(PAGED, q, k_pool, v_pool, None, None, block_table, kl, page_size, scale)
 
 
 def paged_gqa_int8_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
@@ -200,6 +174,4 @@ def paged_gqa_int8_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: t
     _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
     scale = (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
     kl = _kv_len_tensor(kv_len, q.device)
-    return _run("sia_paged_gqa_int8_flash_decode", q,
-                [q, k_pool, v_pool, k_scale_pool, v_scale_pool, block_table, kl],
-                [ctypes.c_int32(page_size)], Hkv, scale)
+    return _run(PAGED_INT8, q, k_pool, v_pool, k_scale_pool, v_scale_pool, block_table, kl, page_size, scale)

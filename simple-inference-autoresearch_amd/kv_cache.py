@@ -19,15 +19,9 @@ Drop-in for ``model/kv_cache.py`` of the reference engine:
 
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
 from . import _lib
-
-
-def _desc_or_null(t):
-    return ctypes.byref(_lib.desc(t)) if t is not None else None
 
 
 def kv_write(k: torch.Tensor, v: torch.Tensor | None, k_dst: torch.Tensor, v_dst: torch.Tensor | None,
@@ -43,14 +37,8 @@ def kv_write(k: torch.Tensor, v: torch.Tensor | None, k_dst: torch.Tensor, v_dst
     An int8 destination is quantised per token and head (scales written to
     ``k_scale_dst`` / ``v_scale_dst``); other destinations receive a cast copy.
     """
-    h = _lib.require_library()
-    if not k.is_cuda:
-        raise ValueError("kv_write runs on the GPU: k must be a CUDA (HIP) tensor")
-    descs = [_desc_or_null(t) for t in (k, v, k_dst, v_dst, k_scale_dst, v_scale_dst, block_table, start_pos)]
-    with torch.cuda.device(k.device):
-        rc = h.sia_kv_write(*descs, ctypes.c_int32(int(start_offset)), ctypes.c_int32(int(page_size)),
-                            ctypes.c_void_p(_lib.stream_handle(k.device)))
-    _lib.check(rc)
+    _lib.gpu_ops().kv_write(k, v, k_dst, v_dst, k_scale_dst, v_scale_dst, block_table, start_pos,
+                            int(start_offset), int(page_size))
 
 
 def rope_kv_write(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor | None, cos: torch.Tensor,
@@ -68,19 +56,8 @@ def rope_kv_write(q: torch.Tensor | None, k: torch.Tensor, v: torch.Tensor | Non
     (rounded to k's dtype) and V are written like :func:`kv_write` writes them;
     the rotated q is returned as ``(B, T, Hq, D)`` (or written to ``q_out``).
     """
-    h = _lib.require_library()
-    if not k.is_cuda:
-        raise ValueError("rope_kv_write runs on the GPU: k must be a CUDA (HIP) tensor")
-    if q is not None and q_out is None:
-        q_out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    descs = [_desc_or_null(t) for t in (q, k, v, cos, sin)]
-    rest = [_desc_or_null(t) for t in (q_out, k_dst, v_dst, k_scale_dst, v_scale_dst, block_table, start_pos)]
-    with torch.cuda.device(k.device):
-        rc = h.sia_rope_kv_write(*descs, ctypes.c_int32(1 if interleaved else 0), *rest,
-                                 ctypes.c_int32(int(start_offset)), ctypes.c_int32(int(page_size)),
-                                 ctypes.c_void_p(_lib.stream_handle(k.device)))
-    _lib.check(rc)
-    return q_out
+    return _lib.gpu_ops().rope_kv_write(q, k, v, cos, sin, k_dst, v_dst, k_scale_dst, v_scale_dst, block_table,
+                                        start_pos, int(start_offset), int(page_size), bool(interleaved), q_out)
 
 
 def quantize_kv_int8(x: torch.Tensor, scale_dtype: torch.dtype = torch.float16):
@@ -92,20 +69,12 @@ def quantize_kv_int8(x: torch.Tensor, scale_dtype: torch.dtype = torch.float16):
     fp16 as in the reference (``model/kv_cache.py:67``); ``scale_dtype=float32``
     keeps it in fp32 (the paged pools' format).
     """
-    h = _lib.require_library()
-    if not x.is_cuda:
-        raise ValueError("quantize_kv_int8 runs on the GPU: x must be a CUDA (HIP) tensor")
+    ops = _lib.gpu_ops()
     if scale_dtype not in (torch.float16, torch.float32):
         raise ValueError("scale_dtype must be float16 or float32")
     src = x if x.stride(-1) == 1 and all((s * x.element_size()) % 16 == 0 for s in x.stride()[:-1]) \
         and x.data_ptr() % 16 == 0 else x.contiguous()
-    xi = torch.empty(x.shape, dtype=torch.int8, device=x.device)
-    scale = torch.empty(x.shape[:-1], dtype=scale_dtype, device=x.device)
-    with torch.cuda.device(x.device):
-        rc = h.sia_quantize_kv_int8(ctypes.byref(_lib.desc(src)), ctypes.byref(_lib.desc(xi)),
-                                    ctypes.byref(_lib.desc(scale)), ctypes.c_void_p(_lib.stream_handle(x.device)))
-    _lib.check(rc)
-    return xi, scale
+    return ops.quantize_kv_int8(src, scale_dtype == torch.float32)
 
 
 def _int32_positions(pos: torch.Tensor) -> torch.Tensor:

@@ -10,7 +10,6 @@ which is kept so callers need no change.
 
 from __future__ import annotations
 
-import ctypes
 import functools
 
 import torch
@@ -24,10 +23,7 @@ _DECODE_DIMS = (64, 128, 256)   # head dims of the decode kernels (single-query 
 @functools.lru_cache(maxsize=256)
 def prefill_workspace_size(batch: int, kv_heads: int, kv_len: int, head_dim: int) -> int:
     """Bytes of device workspace ``sia_attention_flash_fwd`` needs (f16 V^T block images)."""
-    h = _lib.require_library()
-    n = ctypes.c_size_t(0)
-    _lib.check(h.sia_prefill_workspace_size(batch, kv_heads, kv_len, head_dim, ctypes.byref(n)))
-    return int(n.value)
+    return int(_lib.gpu_ops().prefill_workspace_size(batch, kv_heads, kv_len, head_dim))
 
 
 def _supported_view(t: torch.Tensor) -> bool:
@@ -59,32 +55,14 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
         raise AssertionError(f"unsupported head_dim {D}")
     if sm_scale is None:
         sm_scale = 1.0 / (D ** 0.5)
-    h = _lib.require_library()
-    if not q.is_cuda:
-        raise ValueError("attention runs on the GPU: q must be a CUDA (HIP) tensor")
-    if Tq == 1 and Tk >= 1 and D in _DECODE_DIMS and k.dtype == q.dtype and v.dtype == q.dtype:
+    ops = _lib.gpu_ops()
+    if Tq == 1 and Tk >= 1 and D in _DECODE_DIMS and k.dtype == q.dtype and v.dtype == q.dtype and q.is_cuda:
         # one query row sees every key (bottom-right causal == full at Tq = 1):
         # the decode kernels stream K/V once per KV-head group instead of
         # occupying a 256-row prefill work-group per head
-        from .decode import _run
+        from .decode import CONTIG, _run
         kv_len = torch.full((1,), Tk, dtype=torch.int32, device=q.device)
-        out = _run("sia_attention_flash_decode", q, [q, k, v, kv_len], [], Hkv, float(sm_scale))
+        out = _run(CONTIG, q, k, v, None, None, None, kv_len, 0, float(sm_scale))
         return out if out_token_major else out.view(B, Hq, 1, D)
     q, k, v = (t if _supported_view(t) else t.contiguous() for t in (q, k, v))
-    with torch.cuda.device(q.device):
-        if out_token_major:
-            out = torch.empty((B, Tq, Hq, D), dtype=q.dtype, device=q.device)
-            out_view = out.transpose(1, 2)
-        else:
-            out = torch.empty((B, Hq, Tq, D), dtype=q.dtype, device=q.device)
-            out_view = out
-        # float32 calls run on the vector-ALU kernel, which needs no V images
-        nbytes = 0 if q.dtype == torch.float32 else prefill_workspace_size(B, Hkv, Tk, D)
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-        dq, dk, dv, do = (_lib.desc(t) for t in (q, k, v, out_view))
-        rc = h.sia_attention_flash_fwd(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv),
-                                       ctypes.c_int32(1 if causal else 0), ctypes.c_float(float(sm_scale)),
-                                       ctypes.byref(do), ctypes.c_void_p(ws.data_ptr()), ctypes.c_size_t(nbytes),
-                                       ctypes.c_void_p(_lib.stream_handle(q.device)))
-        _lib.check(rc)
-    return out
+    return ops.prefill(q, k, v, bool(causal), float(sm_scale), bool(out_token_major))

@@ -21,7 +21,6 @@ as in the reference kernel.
 
 from __future__ import annotations
 
-import ctypes
 import math
 
 import torch
@@ -79,21 +78,13 @@ def rope_triton(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.
         raise AssertionError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)} in B, T or head_dim")
     if sin.shape[0] != cos.shape[0]:
         raise AssertionError("cos and sin must have the same number of rows")
-    if not (q.is_cuda and k.is_cuda and cos.is_cuda and sin.is_cuda):
-        raise ValueError("rope_triton runs on the GPU: q, k, cos and sin must be CUDA (HIP) tensors")
-    h = _lib.require_library()
+    ops = _lib.gpu_ops()
     if _row_stride(q, T, head_dim) is None:
         q = q.contiguous()
     if _row_stride(k, T, head_dim) is None:
         k = k.contiguous()
-    q_out = torch.empty(B, T, n_heads_q, head_dim, dtype=q.dtype, device=q.device)
-    k_out = torch.empty(B, T, k.shape[2], head_dim, dtype=k.dtype, device=k.device)
-    descs = [ctypes.byref(_lib.desc(t)) for t in (q, k, cos, sin)]
-    with torch.cuda.device(q.device):
-        rc = h.sia_rope_qk(*descs, ctypes.c_int32(1 if interleaved else 0), ctypes.byref(_lib.desc(q_out)),
-                           ctypes.byref(_lib.desc(k_out)), ctypes.c_void_p(_lib.stream_handle(q.device)))
-    _lib.check(rc)
-    return q_out, k_out
+    # outputs are allocated contiguous in C++ (the inputs' shapes and dtypes)
+    return ops.rope_qk(q, k, cos, sin, bool(interleaved))
 
 
 def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):

@@ -12,6 +12,7 @@ from __future__ import annotations
 import importlib
 import os
 import sys
+import zlib
 
 import pytest
 
@@ -45,3 +46,18 @@ def gpu_pkg():
     p = load_pkg()
     p.require_library()
     return p
+
+
+@pytest.fixture(autouse=True)
+def _seed_global_generators(request):
+    """Seed torch's default generators (host and every GPU) per test from its node id.
+
+    Inputs drawn without an explicit generator are then reproducible from the
+    test's name alone; the seed is printed so a failure log names it.
+    """
+    import torch
+
+    seed = zlib.crc32(request.node.nodeid.encode()) & 0x7FFFFFFF
+    torch.manual_seed(seed)   # also seeds every visible GPU's default generator
+    print(f"[seed] {request.node.nodeid}: torch.manual_seed({seed})", flush=True)
+    yield

@@ -81,7 +81,42 @@ def test_no_cpu_fallback(monkeypatch):
     lib_mod = import_module("simple-inference-autoresearch_amd._lib")
     monkeypatch.setattr(lib_mod, "LIB_PATH", "/nonexistent/libsia_attention.so")
     monkeypatch.setattr(lib_mod, "_lib", None)
+    monkeypatch.setattr(lib_mod, "_ops", None)
+    monkeypatch.setattr(lib_mod, "_gpu_checked", False)
     q = torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16)
     k = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16)
     with pytest.raises(pkg.LibraryMissing):
         pkg.attention_flash_decode(q, k, k, torch.tensor([16], dtype=torch.int32))
+
+
+def test_torch_extension_loads_and_binds_the_library(lib):
+    """The thin torch extension loads on the CPU, links the same C ABI and exposes one op per path."""
+    from importlib import import_module
+    lib_mod = import_module("simple-inference-autoresearch_amd._lib")
+    ops = lib_mod.ops()
+    assert ops.abi_version() == lib.sia_abi_version() == 1
+    for name in ("decode", "prefill", "quantize_kv_int8", "kv_write", "rope_kv_write", "rope_qk",
+                 "decode_workspace_size", "prefill_workspace_size"):
+        assert callable(getattr(ops, name)), name
+    n = ctypes.c_size_t(0)
+    assert lib.sia_decode_workspace_size(64, 32, 8, 128, ctypes.byref(n)) == 0
+    assert ops.decode_workspace_size(64, 32, 8, 128) == n.value
+    with pytest.raises(ValueError, match="multiple"):
+        ops.decode_workspace_size(2, 7, 2, 128)
+    with pytest.raises(NotImplementedError):
+        ops.prefill_workspace_size(1, 8, 100, 48)
+
+
+def test_torch_extension_rejects_host_tensors(lib):
+    """Host tensors never reach the kernels: the extension raises before any launch."""
+    from importlib import import_module
+    ops = import_module("simple-inference-autoresearch_amd._lib").ops()
+    q = torch.zeros(1, 8, 1, 128, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 16, 128, dtype=torch.bfloat16)
+    kl = torch.tensor([16], dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.decode(0, q, k, k, None, None, None, kl, 0, 0.1, 0, 0, 0)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.prefill(q, k, k, True, 0.1, False)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.kv_write(k, k, k, k, None, None, None, None, 0, 0)
