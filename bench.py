@@ -78,32 +78,39 @@ def settle(fn, ms: float | None = None) -> None:
         torch.cuda.synchronize()
 
 
-def time_decode(pkg, case, steps: int, warmup: int):
+def time_decode(pkg, cases, steps: int, warmup: int):
     """Clock settle, W untimed calls, then exactly `steps` timed calls.
 
-    Returns (ms per call for the whole call, list of main-kernel ms per call).
+    Call i reads input set i % len(cases) (several sets rotate when one set
+    would fit in the 256 MB MALL).  Returns (ms per call over the back-to-back
+    loop, per-call whole-call ms, per-call main-kernel ms, host µs per call).
+    The whole-call events are recorded at the call boundaries on the launch
+    stream; the main-kernel events by the library around `decode_main` alone.
     """
     import torch
 
-    settle(lambda: run_decode(pkg, case))
-    for _ in range(warmup):
-        run_decode(pkg, case)
+    n = len(cases)
+    settle(lambda: [run_decode(pkg, c) for c in cases])
+    for i in range(warmup):
+        run_decode(pkg, cases[i % n])
     begins = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for e in begins + ends:      # create the underlying hipEvents before handing them to the library
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    for e in begins + ends + marks:   # create the underlying hipEvents before handing them to the library
         e.record()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t0.record()
+    h0 = time.perf_counter()
     for i in range(steps):
+        marks[i].record()
         with pkg.decode_options(main_events=(begins[i], ends[i])):
-            run_decode(pkg, case)
-    t1.record()
+            run_decode(pkg, cases[i % n])
+    marks[steps].record()
+    host_us = (time.perf_counter() - h0) / steps * 1e6
     torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
+    total_ms = marks[0].elapsed_time(marks[steps])
+    calls = [marks[i].elapsed_time(marks[i + 1]) for i in range(steps)]
     kern = [b.elapsed_time(e) for b, e in zip(begins, ends)]
-    return total_ms / steps, kern
+    return total_ms / steps, calls, kern, host_us
 
 
 def cpu_baseline(case, target_s: float):
@@ -171,19 +178,43 @@ def cpu_baseline(case, target_s: float):
     }
 
 
-def bench_decode_config(pkg, case, steps, warmup):
+MALL_BYTES = 256 << 20   # MI355X Infinity Cache
+
+
+def bench_decode_config(pkg, cases, steps, warmup):
     syn = _syn()
-    ms, kern = time_decode(pkg, case, steps, warmup)
-    nbytes = syn.decode_bytes(case)
-    kern_ms = statistics.mean(kern)
+    ms, calls, kern, host_us = time_decode(pkg, cases, steps, warmup)
+    nbytes = syn.decode_bytes(cases[0])
+    k_med, c_med = statistics.median(kern), statistics.median(calls)
+    gbs = lambda t_ms: round(nbytes / (t_ms * 1e-3) / 1e9, 1)
     return {
-        "us_per_call": round(ms * 1e3, 2),
-        "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-        "main_kernel_us": round(kern_ms * 1e3, 2),
-        "main_kernel_GBps": round(nbytes / (kern_ms * 1e-3) / 1e9, 1),
-        "frac_of_hbm_peak": round(nbytes / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "us_per_call": round(c_med * 1e3, 2),
+        "us_per_call_min": round(min(calls) * 1e3, 2),
+        "us_per_call_mean": round(ms * 1e3, 2),
+        "GBps": gbs(c_med),
+        "main_kernel_us": round(k_med * 1e3, 2),
+        "main_kernel_us_min": round(min(kern) * 1e3, 2),
+        "main_kernel_us_mean": round(statistics.mean(kern) * 1e3, 2),
+        "main_kernel_GBps": gbs(k_med),
+        "frac_of_hbm_peak": round(nbytes / (k_med * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "host_us_per_call": round(host_us, 2),
+        "input_sets": len(cases),
+        "input_bytes_total": sum(syn.decode_bytes(c) for c in cases),
         "algorithmic_bytes": nbytes,
+        "statistic": f"median of {steps} calls (min and mean alongside)",
     }
+
+
+def config_cases(syn, name, dev):
+    """Input sets of a decode config: one when it exceeds the MALL twice over, else at
+    least 4 (over 512 MB together) with the same lengths and shapes but other data and
+    page maps, so that no call finds its K/V in the MALL."""
+    first = getattr(syn, name)(dev)
+    nbytes = syn.decode_bytes(first)
+    if nbytes > 2 * MALL_BYTES:
+        return [first]
+    n = max(4, math.ceil(2 * MALL_BYTES / nbytes))
+    return [first] + [syn.config_variant(name, dev, i) for i in range(1, n)]
 
 
 def bench_prefill_config(pkg, steps: int, warmup: int):
@@ -193,22 +224,28 @@ def bench_prefill_config(pkg, steps: int, warmup: int):
     syn = _syn()
     q, k, v = syn.cfg4(torch.device("cuda:0"))
     B, Hq, T, D = q.shape
-    settle(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True))
-    for _ in range(warmup):
-        pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True)
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    for _ in range(steps):
-        pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True)
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    t = time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True), steps, warmup)
+    ms = t["median_ms"]
     flops = syn.prefill_flops(B, Hq, T, D)
     tf = flops / (ms * 1e-3) / 1e12
-    return {"us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 1), "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
-            "algorithmic_flops": flops, "workload": "config 4: causal prefill bf16 B4 T2048 32/8 heads D128"}
+    return {**_timing_fields(t), "TFLOPs": round(tf, 1), "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "algorithmic_flops": flops, "workload": "config 4: causal prefill bf16 B4 T2048 32/8 heads D128",
+            "statistic": f"median of {steps} calls"}
+
+
+def bench_config1(pkg, steps: int, warmup: int):
+    """Config 1 on the GPU: contiguous fp32 decode B1, 32/8 heads, D64, ctx 512 (seed 0),
+    scale 1/8, through attention_flash_decode (the fp32 vector-ALU path)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    q, k, v = (t.to(dev) for t in _syn().cfg1())
+    kv_len = torch.tensor([512], dtype=torch.int32, device=dev)
+    t = time_calls(lambda: pkg.attention_flash_decode(q, k, v, kv_len, 0.125), steps, warmup)
+    nbytes = 2 * 8 * 512 * 64 * 4 + 2 * 32 * 64 * 4
+    gbs = nbytes / (t["median_ms"] * 1e-3) / 1e9
+    return {**_timing_fields(t), "GBps": round(gbs, 1), "algorithmic_bytes": nbytes,
+            "workload": "config 1: contiguous fp32 decode B1 32/8 heads D64 ctx 512 (2.1 MB: launch-bound)"}
 
 
 def rope_bytes(B: int, T: int, Hq: int, Hkv: int, D: int, es: int = 2) -> int:
@@ -231,21 +268,11 @@ def bench_rope_config(pkg, steps: int, warmup: int):
         q = torch.randn(B, T, 32, 128, device=dev, dtype=torch.bfloat16, generator=g)
         k = torch.randn(B, T, 8, 128, device=dev, dtype=torch.bfloat16, generator=g)
         cos, sin = rf.get(T, start_pos=0 if T > 1 else 4000, dtype=torch.bfloat16)
-        settle(lambda: pkg.rope_triton(q, k, cos, sin))
-        for _ in range(warmup):
-            pkg.rope_triton(q, k, cos, sin)
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(steps):
-            pkg.rope_triton(q, k, cos, sin)
-        e1.record()
-        torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
+        t = time_calls(lambda: pkg.rope_triton(q, k, cos, sin), steps, warmup)
+        ms = t["median_ms"]
         nbytes = rope_bytes(B, T, 32, 8, 128)
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out[label] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+        out[label] = {**_timing_fields(t), "GBps": round(gbs, 1),
                       "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
     out["workload"] = "fused q/k RoPE bf16, 32/8 heads D128, split-half, Llama 3 tables"
     out["rope_kv_write"] = bench_rope_kv_write(pkg, rf, steps, warmup)
@@ -306,22 +333,15 @@ def bench_rope_kv_write(pkg, rf, steps: int, warmup: int):
             pkg.kv_write(kr.transpose(1, 2), v.contiguous().transpose(1, 2), kc, vc, ks, vs, **kw)
 
         res = {}
+        host = {}
         for name, fn in (("fused", fused), ("rope_then_write", unfused)):
-            settle(fn)
-            for _ in range(warmup):
-                fn()
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            e0.record()
-            for _ in range(steps):
-                fn()
-            e1.record()
-            torch.cuda.synchronize()
-            res[name] = round(e0.elapsed_time(e1) / steps * 1e3, 2)
+            t = time_calls(fn, steps, warmup)
+            res[name] = round(t["median_ms"] * 1e3, 2)
+            host[name] = round(t["host_us"], 2)
         nbytes = rope_kv_write_bytes(B, T, Hq, Hkv, D)
         gbs = nbytes / (res["fused"] * 1e-6) / 1e9
         out[label] = {"fused_us_per_call": res["fused"], "rope_then_write_us_per_call": res["rope_then_write"],
+                      "fused_host_us_per_call": host["fused"],
                       "fused_GBps": round(gbs, 1), "fused_frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
                       "algorithmic_bytes": nbytes}
     out["workload"] = ("RoPE of q, k fused into the int8 KV write (bf16 q/k/v slices of one qkv buffer, "
@@ -329,22 +349,44 @@ def bench_rope_kv_write(pkg, rf, steps: int, warmup: int):
     return out
 
 
-def _time_calls(fn, steps: int, warmup: int) -> float:
-    """Mean milliseconds per call of `fn` over `steps` back-to-back calls (after settle + warm-up)."""
+def time_calls(fn, steps: int, warmup: int) -> dict:
+    """Clock settle, W untimed calls, then two timed passes of `steps` back-to-back calls.
+
+    Pass 1 records a HIP event on the current stream at every call boundary:
+    the median and min milliseconds per call.  Pass 2 records events only
+    around the whole loop: the mean milliseconds per call of an unbroken
+    sequence of calls, and the host microseconds to issue one call (an event
+    record itself costs the host about 4 us, so pass 1 overstates the wall
+    time of calls whose kernels are shorter than their host cost)."""
     import torch
 
     settle(fn)
     for _ in range(warmup):
         fn()
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        marks[i].record()
+        fn()
+    marks[steps].record()
+    torch.cuda.synchronize()
+    per = [marks[i].elapsed_time(marks[i + 1]) for i in range(steps)]
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     e0.record()
+    h0 = time.perf_counter()
     for _ in range(steps):
         fn()
+    host_us = (time.perf_counter() - h0) / steps * 1e6
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    return {"median_ms": statistics.median(per), "min_ms": min(per),
+            "mean_ms": e0.elapsed_time(e1) / steps, "host_us": host_us}
+
+
+def _timing_fields(t: dict) -> dict:
+    return {"us_per_call": round(t["median_ms"] * 1e3, 2), "us_per_call_min": round(t["min_ms"] * 1e3, 2),
+            "us_per_call_back_to_back": round(t["mean_ms"] * 1e3, 2), "host_us_per_call": round(t["host_us"], 2)}
 
 
 def bench_qwen35_config(pkg, steps: int, warmup: int):
@@ -362,20 +404,22 @@ def bench_qwen35_config(pkg, steps: int, warmup: int):
     k = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
     v = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
     kv_len = torch.tensor([S], dtype=torch.int32, device=dev)
-    ms = _time_calls(lambda: pkg.attention_flash_decode(q, k, v, kv_len), steps, warmup)
+    t = time_calls(lambda: pkg.attention_flash_decode(q, k, v, kv_len), steps, warmup)
+    ms = t["median_ms"]
     nbytes = 2 * B * Hkv * S * D * 2 + 2 * B * Hq * D * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
-    out["decode_B32_ctx4096"] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(gbs, 1),
+    out["decode_B32_ctx4096"] = {**_timing_fields(t), "GBps": round(gbs, 1),
                                  "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
     del q, k, v
     T = 4096
     q = (torch.randn(1, Hq, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
     k = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
     v = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
-    ms = _time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True), steps, warmup)
+    t = time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True), steps, warmup)
+    ms = t["median_ms"]
     flops = _syn().prefill_flops(1, Hq, T, D)
     tf = flops / (ms * 1e-3) / 1e12
-    out["prefill_B1_T4096"] = {"us_per_call": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+    out["prefill_B1_T4096"] = {**_timing_fields(t), "TFLOPs": round(tf, 1),
                                "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": flops}
     out["workload"] = "Qwen3.5 full attention: head_dim 256, 16/4 heads, bf16, contiguous cache"
     return out
@@ -464,11 +508,12 @@ def main(argv=None):
         print(f"[bench] cfg4: {r}", file=sys.stderr, flush=True)
         print(json.dumps({"config": "cfg4", **r}), flush=True)
         return 0
-    case = getattr(syn, args.config)(dev)
+    cases = config_cases(syn, args.config, dev)
+    case = cases[0]
     torch.cuda.synchronize()
-    print(f"[bench] {args.config}: inputs resident ({syn.decode_bytes(case)/1e9:.3f} GB algorithmic)",
-          file=sys.stderr, flush=True)
-    head = bench_decode_config(pkg, case, args.steps, args.warmup)
+    print(f"[bench] {args.config}: inputs resident ({syn.decode_bytes(case)/1e9:.3f} GB algorithmic, "
+          f"{len(cases)} rotating set(s))", file=sys.stderr, flush=True)
+    head = bench_decode_config(pkg, cases, args.steps, args.warmup)
     print(f"[bench] {args.config}: {head}", file=sys.stderr, flush=True)
 
     result = {
@@ -479,8 +524,12 @@ def main(argv=None):
         "steps": args.steps,
         "warmup": args.warmup,
         "clock_settle_ms": args.settle_ms,
-        "ms_per_step": round(head["us_per_call"] / 1e3, 5),
+        "ms_per_step": round(head["us_per_call_mean"] / 1e3, 5),
         "us_per_call": head["us_per_call"],
+        "us_per_call_min": head["us_per_call_min"],
+        "us_per_call_mean": head["us_per_call_mean"],
+        "host_us_per_call": head["host_us_per_call"],
+        "statistic": head["statistic"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -504,6 +553,8 @@ def main(argv=None):
             "traffic": None,
             "kernel": "decode_main",
             "kernel_us": head["main_kernel_us"],
+            "kernel_us_min": head["main_kernel_us_min"],
+            "statistic": "median of the per-call HIP events around decode_main",
         },
     }
     tr = load_traffic(f"decode_main_{args.config}")
@@ -513,20 +564,22 @@ def main(argv=None):
 
     if not args.no_others and args.config == "cfg3":
         others = {}
-        del case
+        del case, cases
         torch.cuda.empty_cache()
         for name in ("cfg2", "cfg5"):
-            c = getattr(syn, name)(dev)
+            cs = config_cases(syn, name, dev)
             torch.cuda.synchronize()
-            others[name] = bench_decode_config(pkg, c, max(20, args.steps // 2), args.warmup)
+            others[name] = bench_decode_config(pkg, cs, max(50, args.steps // 2), args.warmup)
             print(f"[bench] {name}: {others[name]}", file=sys.stderr, flush=True)
-            del c
+            del cs
             torch.cuda.empty_cache()
-        others["cfg4"] = bench_prefill_config(pkg, max(20, args.steps // 2), args.warmup)
+        others["cfg1"] = bench_config1(pkg, max(50, args.steps // 2), args.warmup)
+        print(f"[bench] cfg1: {others['cfg1']}", file=sys.stderr, flush=True)
+        others["cfg4"] = bench_prefill_config(pkg, max(50, args.steps // 2), args.warmup)
         print(f"[bench] cfg4: {others['cfg4']}", file=sys.stderr, flush=True)
-        others["rope"] = bench_rope_config(pkg, max(20, args.steps // 2), args.warmup)
+        others["rope"] = bench_rope_config(pkg, max(50, args.steps // 2), args.warmup)
         print(f"[bench] rope: {others['rope']}", file=sys.stderr, flush=True)
-        others["qwen35"] = bench_qwen35_config(pkg, max(20, args.steps // 2), args.warmup)
+        others["qwen35"] = bench_qwen35_config(pkg, max(50, args.steps // 2), args.warmup)
         print(f"[bench] qwen35: {others['qwen35']}", file=sys.stderr, flush=True)
         result["other_configs"] = others
         case = None

@@ -133,6 +133,18 @@ def cfg5(device) -> PagedCase:
                       q_dtype=torch.bfloat16)
 
 
+def config_variant(name: str, device, i: int) -> PagedCase:
+    """Input set i (>= 1) of decode config `name`: the config's lengths and shapes with
+    other K/V data and another page permutation (seed + 1000 i), so that timing can
+    rotate through sets whose total exceeds the MALL."""
+    ctx = {"cfg2": cfg2_lengths(), "cfg3": [8192] * 64, "cfg5": cfg5_lengths()}[name]
+    kw = {"cfg2": dict(Hq=32, Hkv=8, D=128, page=16, seed=1, kv="fp16", q_dtype=torch.float16),
+          "cfg3": dict(Hq=32, Hkv=8, D=128, page=16, seed=2, kv="int8", q_dtype=torch.bfloat16, per_seq_len=False),
+          "cfg5": dict(Hq=64, Hkv=8, D=128, page=16, seed=4, kv="int8", q_dtype=torch.bfloat16)}[name]
+    kw["seed"] += 1000 * i
+    return paged_case(ctx, device=device, **kw)
+
+
 def cfg1():
     g = torch.Generator().manual_seed(0)
     q = torch.randn((1, 32, 1, 64), generator=g)
