@@ -137,6 +137,25 @@ int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_poo
                                     void* workspace, size_t workspace_bytes,
                                     const sia_decode_options* opts, void* stream);
 
+/* sia_paged_gqa_int8_flash_decode without a workspace argument: no
+ * counterpart in the reference.  It is for callers that cannot allocate
+ * device memory (code under HIP-graph capture, serving loops and harnesses
+ * that forbid hipMalloc).  The split-K partials go to a static device array
+ * of SIA_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until
+ * the process ends; nothing is allocated, freed or cleared per call.  A
+ * geometry whose partials for one work-group per CU do not fit that array
+ * fails with SIA_ERR_WORKSPACE (no valid head_dim/GQA shape does at 64 MiB).
+ * Every call on a GPU shares that GPU's array, so calls that overlap on one
+ * GPU (concurrent streams, threads) race: serialise them.  Arguments,
+ * results and errors are otherwise those of sia_paged_gqa_int8_flash_decode. */
+#define SIA_NOALLOC_SCRATCH_BYTES (64u << 20)
+int sia_paged_gqa_int8_flash_decode_noalloc(const sia_tensor* q, const sia_tensor* k_pool,
+                                            const sia_tensor* v_pool, const sia_tensor* k_scale_pool,
+                                            const sia_tensor* v_scale_pool,
+                                            const sia_tensor* block_table, const sia_tensor* kv_len,
+                                            int32_t page_size, float sm_scale, const sia_tensor* out,
+                                            const sia_decode_options* opts, void* stream);
+
 /* Replaces attention_flash_triton (kernels/attention_kernel.py:235-305).
  * q (B,Hq,Tq,D), k,v (B,Hkv,Tk,D): f16|bf16|f32 views (one dtype), head_dim contiguous,
  * 16-byte aligned rows; out (B,Hq,Tq,D) view in q's dtype -- a transposed

@@ -2,6 +2,8 @@
 #include <math.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "attn_f32.hpp"
 #include "decode_launch.hpp"
 #include "host_util.hpp"
@@ -318,6 +320,35 @@ int decode_any(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, co
   return dispatch(L, k->dtype);
 }
 
+// Split-K workspace of sia_paged_gqa_int8_flash_decode_noalloc: a static
+// device array, one copy per GPU, held until the process ends.  Host code
+// never passes `scratch` itself (its name is a host-side stand-in, not a
+// device address): the device address of each GPU's copy comes from
+// hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t kScratchBytes = (size_t)SIA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+
+// Device address of this GPU's scratch (looked up on its first use).
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+    return fail(SIA_ERR_DEVICE, "no HIP device is current");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(SIA_ERR_DEVICE, "cannot resolve the static decode scratch on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SIA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -380,6 +411,33 @@ int sia_paged_attention_flash_decode(const sia_tensor* q, const sia_tensor* k_po
   if (block_table == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "block_table is NULL");
   return decode_any(q, k_pool, v_pool, nullptr, nullptr, block_table, kv_len, page_size, sm_scale, out,
                     workspace, workspace_bytes, opts, stream, false);
+}
+
+int sia_paged_gqa_int8_flash_decode_noalloc(const sia_tensor* q, const sia_tensor* k_pool, const sia_tensor* v_pool,
+                                            const sia_tensor* k_scale_pool, const sia_tensor* v_scale_pool,
+                                            const sia_tensor* block_table, const sia_tensor* kv_len,
+                                            int32_t page_size, float sm_scale, const sia_tensor* out,
+                                            const sia_decode_options* opts, void* stream) {
+  if (block_table == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "block_table is NULL");
+  if (k_pool == nullptr || q == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "q or k_pool is NULL");
+  if (q->ndim != 4 || k_pool->ndim != 4) return fail(SIA_ERR_INVALID_ARGUMENT, "q and k_pool must have 4 dims");
+  // the split-K partials of at least one work-group per CU must fit the static scratch
+  Geometry g;
+  int rc = geometry(q->shape[0], q->shape[1], k_pool->shape[1], q->shape[3], g);
+  if (rc) return rc;
+  const int cus = device_info().cus > 0 ? device_info().cus : 256;
+  const size_t need = plan_bytes(g.B) + item_bytes(g) * 2 * (size_t)cus;
+  if (need > kScratchBytes)
+    return fail(SIA_ERR_WORKSPACE,
+                "this geometry needs %zu bytes of split-K scratch; the static scratch of the no-allocation entry "
+                "point holds %zu (use sia_paged_gqa_int8_flash_decode with a workspace)",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_for_current_device(&ws))) return rc;
+  // nothing in the scratch needs to start at zero: every call writes the plan
+  // and each partial slot before reading it
+  return decode_any(q, k_pool, v_pool, k_scale_pool, v_scale_pool, block_table, kv_len, page_size, sm_scale, out,
+                    ws, kScratchBytes, opts, stream, true);
 }
 
 int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_pool, const sia_tensor* v_pool,
