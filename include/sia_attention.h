@@ -227,9 +227,12 @@ int sia_kv_write(const sia_tensor* k, const sia_tensor* v, const sia_tensor* k_d
  * is rounded to k's dtype, then written like sia_kv_write writes k (cast, or
  * int8 with a per-token-per-head scale); v is written unrotated; q_out
  * (B, T, Hq, D), any strides with unit head_dim, receives the rotated q in
- * q's dtype.  K/V rows whose position is outside the destination or the
- * table are skipped; q rows whose position is outside the table are written
- * as zeros. */
+ * q's dtype.  Without start_pos (positions known on the host) every
+ * position must have a table row, else SIA_ERR_INVALID_ARGUMENT.  With
+ * start_pos (positions read on the device, where no error can be returned),
+ * K/V rows whose position is outside the destination or the table are
+ * skipped and q rows whose position is outside the table are written as
+ * zeros: size the tables to the cache length. */
 int sia_rope_kv_write(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, const sia_tensor* cos,
                       const sia_tensor* sin, int32_t interleaved, const sia_tensor* q_out, const sia_tensor* k_dst,
                       const sia_tensor* v_dst, const sia_tensor* k_scale_dst, const sia_tensor* v_scale_dst,

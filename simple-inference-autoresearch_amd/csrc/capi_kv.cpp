@@ -216,6 +216,11 @@ int sia_rope_kv_write(const sia_tensor* q, const sia_tensor* k, const sia_tensor
   if (cos->stride[1] != 1 || sin->stride[1] != 1 || cos->stride[0] != sin->stride[0])
     return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin must be unit-stride rows with one row stride");
   if (cos->shape[0] <= 0 || cos->shape[0] > 0x7fffffff) return fail(SIA_ERR_INVALID_ARGUMENT, "bad table row count");
+  // positions known on the host must have a table row (device positions are
+  // checked on the device: rows outside the table are skipped / zeroed)
+  if (start_pos == nullptr && (start_pos_host < 0 || (int64_t)start_pos_host + T > cos->shape[0]))
+    return fail(SIA_ERR_INVALID_ARGUMENT, "positions [%d, %lld) need cos/sin rows the %lld-row tables do not have",
+                start_pos_host, (long long)start_pos_host + T, (long long)cos->shape[0]);
   a.rope = interleaved ? 2 : 1;
   a.cs = (const char*)cos->data;
   a.sn = (const char*)sin->data;

@@ -54,12 +54,18 @@ def llama_paged_cache_builder(config, *, max_batch: int, max_seq_len: int, dtype
 
 
 def _padding_free(attention_mask) -> bool:
-    """True when the mask the model passes carries no padding (None or a 2D mask of ones)."""
-    if attention_mask is None:
-        return True
-    if attention_mask.dim() == 2:
-        return bool(torch.all(attention_mask != 0))
-    return False
+    """True when the model passes no mask: the un-padded case.
+
+    The mask builder registered with this function (transformers'
+    ``flash_attention_2`` one) already returns ``None`` for a batch without
+    padding, once per forward; any mask it does return marks padded keys (or
+    a static cache's unfilled slots), which no kernel here handles.  So the
+    decision needs no look at the mask's values: no device-to-host copy per
+    layer, and a decode step stays capturable in a HIP graph.  The
+    reference's Qwen3.5 plugin calls the backbone without a mask
+    (``model/qwen35_plugin.py:396-402``), which is the ``None`` case.
+    """
+    return attention_mask is None
 
 
 def sia_attention_forward(module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, attention_mask,
@@ -78,7 +84,8 @@ def sia_attention_forward(module, query: torch.Tensor, key: torch.Tensor, value:
     if kwargs.get("sliding_window") is not None or kwargs.get("softcap") is not None:
         raise NotImplementedError("sliding-window / soft-capped attention is not supported")
     if not _padding_free(attention_mask):
-        raise NotImplementedError("padded batches (a non-trivial attention mask) are not supported")
+        raise NotImplementedError("an attention mask (padded batch or static-cache slots) is not supported; "
+                                  "un-padded batches reach this function with attention_mask=None")
     causal = getattr(module, "is_causal", True) if is_causal is None else bool(is_causal)
     out = attention_flash_triton(query, key, value, causal=causal, sm_scale=scaling, out_token_major=True)
     return out, None

@@ -59,8 +59,45 @@ def test_attention_function_rejects_padding(gpu_pkg):
     mask = torch.tensor([[0, 1, 1, 1]], device=DEV)
     with pytest.raises(NotImplementedError):
         _plugins().sia_attention_forward(_Module(), q, k, k, mask, scaling=0.125)
+    # any mask the registered builder returns marks padding: rejected without reading it
+    with pytest.raises(NotImplementedError):
+        _plugins().sia_attention_forward(_Module(), q, k, k, torch.ones(1, 4, dtype=torch.bool, device=DEV),
+                                         scaling=0.125)
     with pytest.raises(NotImplementedError):
         _plugins().sia_attention_forward(_Module(), q, k, k, None, dropout=0.1)
+
+
+def test_attention_function_decode_step_in_hip_graph(gpu_pkg):
+    """A Qwen3.5 decode step (Tq = 1, head_dim 256, 8/2 heads) through sia_attention_forward,
+    captured once in a HIP graph and replayed with new query and cache contents: every
+    replay equals the eager call bit for bit and the oracle within 2e-3 or one ulp."""
+    announce("sia_attention_forward decode step under HIP-graph capture")
+    B, Hq, Hkv, S, D = 2, 8, 2, 300, 256
+    g = torch.Generator(device=DEV).manual_seed(77)
+    q = (torch.randn(B, Hq, 1, D, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(B, Hkv, S, D, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(B, Hkv, S, D, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    fwd = _plugins().sia_attention_forward
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fwd(_Module(), q, k, v, None, scaling=D ** -0.5)          # warm-up outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out, _ = fwd(_Module(), q, k, v, None, scaling=D ** -0.5)
+    for i in range(3):
+        q.copy_((torch.randn(B, Hq, 1, D, generator=g, device=DEV) * 0.5).to(torch.bfloat16))
+        v[:, :, 17 * i] = (torch.randn(B, Hkv, D, generator=g, device=DEV)).to(torch.bfloat16)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager, _ = fwd(_Module(), q, k, v, None, scaling=D ** -0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from the eager call"
+        ref = O.flash_attention(f64(q), f64(k), f64(v), True, D ** -0.5)
+        got = f64(out.transpose(1, 2))
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -24))) - 7)
+        assert (np.abs(got - ref) <= np.maximum(2e-3, ulp)).all(), np.abs(got - ref).max()
 
 
 def test_qwen35_full_attention_model(gpu_pkg):

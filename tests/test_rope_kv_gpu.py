@@ -291,6 +291,12 @@ def test_invalid_arguments(gpu_pkg):
         gpu_pkg.rope_kv_write(q, k, v, cos[:, :20], sin[:, :20], kc, torch.zeros_like(kc))
     with pytest.raises(ValueError, match="share a dtype"):
         gpu_pkg.rope_kv_write(q.float(), k, v, cos, sin, kc, torch.zeros_like(kc))
+    # host-known positions past the 4-row tables are an error (nothing written)
+    kc8 = torch.zeros(1, 1, 8, 64, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(ValueError, match="rows"):
+        gpu_pkg.rope_kv_write(q, k, v, cos, sin, kc8, torch.zeros_like(kc8), start_offset=4)
+    torch.cuda.synchronize()
+    assert not kc8.any()
 
 
 def test_rope_decode_step_hip_graph_contiguous(gpu_pkg):
