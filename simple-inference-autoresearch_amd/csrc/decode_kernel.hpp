@@ -370,6 +370,11 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
   constexpr int KSTEPS = D / 32;
   constexpr int E = D / 16;
   constexpr bool kInt8 = std::is_same<KV, I8>::value;
+  // P enters the PV product in the MFMA type.  bf16 keeps 8 significant bits,
+  // so P is split into a bf16 pair (hi + lo, two MFMAs); f16's 11 bits keep
+  // the output within the fp16 bar with one (a rounding of 2^-12 relative per
+  // weight); int8 V takes P' in f16 (one MFMA).
+  constexpr bool kPSplit = !kInt8 && std::is_same<MT, BF16>::value;
 
   float s[4];
   if constexpr (kInt8) {
@@ -436,8 +441,10 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
   } else {
     pop[0] = pack2(MT{}, p[0], p[1]);
     pop[1] = pack2(MT{}, p[2], p[3]);
-    pop_lo[0] = pack2(MT{}, p[0] - lo_f32(MT{}, pop[0]), p[1] - hi_f32(MT{}, pop[0]));
-    pop_lo[1] = pack2(MT{}, p[2] - lo_f32(MT{}, pop[1]), p[3] - hi_f32(MT{}, pop[1]));
+    if constexpr (kPSplit) {
+      pop_lo[0] = pack2(MT{}, p[0] - lo_f32(MT{}, pop[0]), p[1] - hi_f32(MT{}, pop[0]));
+      pop_lo[1] = pack2(MT{}, p[2] - lo_f32(MT{}, pop[1]), p[3] - hi_f32(MT{}, pop[1]));
+    }
   }
   if (rescale) {
     st.l *= alpha;
@@ -450,7 +457,7 @@ __device__ __forceinline__ void compute_tile(const Tile<D, KV, ST>& c, const u32
   for (int e = 0; e < E; ++e) {
     const u32x2 va = v_operand<D, KV, ST>(c, e);
     st.acc[e] = mfma16x16x16(MT{}, va, pop, st.acc[e]);
-    if constexpr (!kInt8) st.acc[e] = mfma16x16x16(MT{}, va, pop_lo, st.acc[e]);
+    if constexpr (kPSplit) st.acc[e] = mfma16x16x16(MT{}, va, pop_lo, st.acc[e]);
   }
 }
 
