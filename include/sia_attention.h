@@ -171,6 +171,27 @@ int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_
                             float sm_scale, const sia_tensor* out, void* workspace, size_t workspace_bytes,
                             void* stream);
 
+/* sia_attention_flash_fwd with the rotary embedding of q applied as q is
+ * loaded: replaces rope_triton (kernels/rope_kernel.py:261-285) on q followed
+ * by attention_flash_triton (kernels/attention_kernel.py:235-305), the pair
+ * the reference's prefill runs (ops/attention.py:291-292 then 327-330), in
+ * one launch with no rotated copy of q.  k must already hold
+ * rotated keys (sia_rope_kv_write with q NULL writes them to the cache).
+ * Query row i of sequence b sits at position p = start_pos_host +
+ * start_pos[b] + i, start_pos an int32 device tensor ((1,)/() shared or (B,)
+ * per sequence, read on the device) or NULL (p = start_pos_host + i, checked
+ * against the table rows on the host: SIA_ERR_INVALID_ARGUMENT).  cos, sin
+ * as for sia_rope_qk (row p of the table, first D/2 columns, 16-byte aligned
+ * rows); interleaved 0: pairs (i, i + D/2), 1: pairs (2i, 2i + 1).  The
+ * rotation is sia_rope_qk's arithmetic and rounding, so the result equals
+ * sia_rope_qk followed by sia_attention_flash_fwd bit for bit.  A device
+ * position outside the table rotates q to zeros.  float16/bfloat16 only
+ * (float32 q: SIA_ERR_UNSUPPORTED); workspace as for sia_attention_flash_fwd. */
+int sia_attention_flash_fwd_rope(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, const sia_tensor* cos,
+                                 const sia_tensor* sin, int32_t interleaved, const sia_tensor* start_pos,
+                                 int32_t start_pos_host, int32_t causal, float sm_scale, const sia_tensor* out,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes sia_attention_flash_fwd needs for v of shape
  * (batch, kv_heads, kv_len, head_dim).  No reference counterpart: the
  * reference's Triton launch allocates nothing (kernels/attention_kernel.py:296). */

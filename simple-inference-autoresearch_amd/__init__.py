@@ -23,7 +23,7 @@ from .decode import (
     paged_attention_flash_decode,
     paged_gqa_int8_flash_decode,
 )
-from .prefill import attention_flash_triton, prefill_workspace_size
+from .prefill import attention_flash_triton, prefill_workspace_size, rope_attention_flash_triton
 from .kv_cache import KVCache, kv_write, quantize_kv_int8, rope_kv_write
 from .paged_kv_cache import PagedKVCache
 from .rope import RopeFrequencies, apply_rope, rope_triton
@@ -45,6 +45,7 @@ __all__ = [
     "kv_write",
     "quantize_kv_int8",
     "attention_flash_triton",
+    "rope_attention_flash_triton",
     "SiaError",
     "attention_flash_decode",
     "attention_flash_decode_int8",

@@ -105,6 +105,7 @@ _SIGNATURES = {
     "sia_paged_gqa_int8_flash_decode_noalloc": [_P, _P, _P, _P, _P, _P, _P, _I32, _F, _P,
                                                 ctypes.POINTER(DecodeOptions), _VP],
     "sia_attention_flash_fwd": [_P, _P, _P, _I32, _F, _P, _VP, _SZ, _VP],
+    "sia_attention_flash_fwd_rope": [_P, _P, _P, _P, _P, _I32, _P, _I32, _I32, _F, _P, _VP, _SZ, _VP],
     "sia_prefill_workspace_size": [_I64, _I64, _I64, _I64, ctypes.POINTER(_SZ)],
     "sia_quantize_kv_int8": [_P, _P, _P, _VP],
     "sia_kv_write": [_P, _P, _P, _P, _P, _P, _P, _P, _I32, _I32, _VP],

@@ -63,22 +63,62 @@ int prefill_f32(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, i
   return launch_attn_f32(L);
 }
 
-}  // namespace
+// Rotary tables of the fused entry point (NULL cos: no rotation).
+struct RopeIn {
+  const sia_tensor* cos;
+  const sia_tensor* sin;
+  const sia_tensor* start_pos;
+  int32_t start_host;
+  int32_t interleaved;
+};
 
-extern "C" int sia_prefill_workspace_size(int64_t batch, int64_t kv_heads, int64_t kv_len, int64_t head_dim,
-                                          size_t* bytes) {
-  if (bytes == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "bytes is NULL");
-  if (batch <= 0 || kv_heads <= 0 || kv_len < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "bad sizes");
-  if (!head_dim_ok(head_dim))
-    return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (16, 32, 64, 128, 256)",
-                (long long)head_dim);
-  *bytes = (size_t)image_bytes(batch, kv_heads, kv_len, head_dim);
+// Checks the tables and positions against q (B, Hq, Tq, D) and fills the
+// rotation fields of the kernel arguments.
+int setup_rope(const RopeIn& r, int64_t B, int64_t Tq, int64_t D, PrefillArgs& a) {
+  const sia_tensor* cos = r.cos;
+  const sia_tensor* sin = r.sin;
+  if (cos == nullptr || sin == nullptr || cos->data == nullptr || sin->data == nullptr || cos->ndim != 2 ||
+      sin->ndim != 2)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos and sin must be (rows, width) tables");
+  if (cos->shape[0] != sin->shape[0] || cos->shape[1] != sin->shape[1])
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos and sin must have identical shape");
+  if (cos->shape[1] != D && cos->shape[1] != D / 2)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin last dim must be head_dim (%lld) or head_dim/2 (%lld)",
+                (long long)D, (long long)(D / 2));
+  if (cos->dtype != sin->dtype || (cos->dtype != SIA_F16 && cos->dtype != SIA_BF16 && cos->dtype != SIA_F32))
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos and sin must share a float dtype");
+  if (cos->stride[1] != 1 || sin->stride[1] != 1 || cos->stride[0] != sin->stride[0])
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin must be unit-stride rows with one row stride");
+  if (cos->shape[0] <= 0 || cos->shape[0] > 0x7fffffff) return fail(SIA_ERR_INVALID_ARGUMENT, "bad table row count");
+  a.tab_rs = cos->stride[0] * elem_size(cos->dtype);
+  if (!aligned16(cos->data) || !aligned16(sin->data) || a.tab_rs % 16 != 0)
+    return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin must be 16-byte aligned with 16-byte multiple row strides");
+  if (r.start_pos != nullptr) {
+    const sia_tensor* sp = r.start_pos;
+    if (sp->data == nullptr || sp->dtype != SIA_I32 || sp->ndim > 1)
+      return fail(SIA_ERR_INVALID_ARGUMENT, "start_pos must be an int32 scalar, (1,) or (B,) tensor");
+    const int64_t n = sp->ndim == 0 ? 1 : sp->shape[0];
+    if (n != 1 && n != B) return fail(SIA_ERR_INVALID_ARGUMENT, "start_pos must have 1 or B elements");
+    if (n == B && B > 1 && sp->stride[0] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "start_pos must be contiguous");
+    a.start_pos = (const int32_t*)sp->data;
+    a.pos_per_seq = n == B && B > 1;
+  } else if (r.start_host < 0 || (int64_t)r.start_host + Tq > cos->shape[0]) {
+    // positions known on the host must have a table row; device positions
+    // outside the table rotate q to zeros
+    return fail(SIA_ERR_INVALID_ARGUMENT, "positions [%d, %lld) need cos/sin rows the %lld-row tables do not have",
+                r.start_host, (long long)r.start_host + Tq, (long long)cos->shape[0]);
+  }
+  a.start_host = r.start_host;
+  a.cs = (const char*)cos->data;
+  a.sn = (const char*)sin->data;
+  a.Tc = (int32_t)cos->shape[0];
+  a.tab_dt = cos->dtype;
+  a.interleaved = r.interleaved != 0;
   return SIA_OK;
 }
 
-extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
-                                       float sm_scale, const sia_tensor* out, void* workspace,
-                                       size_t workspace_bytes, void* stream) {
+int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal, float sm_scale,
+              const sia_tensor* out, void* workspace, size_t workspace_bytes, void* stream, const RopeIn* rope) {
   int rc;
   if ((rc = check4(q, "q")) || (rc = check4(k, "k")) || (rc = check4(v, "v")) || (rc = check4(out, "out"))) return rc;
   if (q->dtype != SIA_F16 && q->dtype != SIA_BF16 && q->dtype != SIA_F32)
@@ -103,7 +143,11 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
     return fail(SIA_ERR_UNSUPPORTED, "k token stride %lld bytes: expected [%lld, 2^31/64)", (long long)k_sn,
                 (long long)(2 * D));
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return fail(SIA_ERR_INVALID_ARGUMENT, "sm_scale must be positive");
-  if (q->dtype == SIA_F32) return prefill_f32(q, k, v, causal, sm_scale, out, stream);
+  if (q->dtype == SIA_F32) {
+    if (rope != nullptr)
+      return fail(SIA_ERR_UNSUPPORTED, "the rotary prologue runs on the float16/bfloat16 MFMA path only");
+    return prefill_f32(q, k, v, causal, sm_scale, out, stream);
+  }
   const int64_t need = image_bytes(B, Hkv, Tk, D);
   if (need > 0 && (workspace == nullptr || (uintptr_t)workspace % 256 || workspace_bytes < (size_t)need))
     return fail(SIA_ERR_WORKSPACE, "prefill workspace missing, misaligned or smaller than %lld bytes",
@@ -111,7 +155,6 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   const DeviceInfo& dev = device_info();
   if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
   if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
-  if (Tq == 0) return SIA_OK;
 
   PrefillLaunch L;
   memset(&L, 0, sizeof(L));
@@ -129,6 +172,7 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   const int64_t groups = (int64_t)a.nqblk * B * Hkv;   // work-groups come in runs of G sharing a KV head
   if (groups * a.G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "grid too large");
   a.remap = groups % 8 == 0;
+  if (rope != nullptr && (rc = setup_rope(*rope, B, Tq, D, a))) return rc;
 
   PackArgs& p = L.pack;
   p.v = (const char*)v->data; p.v_sb = bstride(v, 0); p.v_sh = bstride(v, 1); p.v_sn = bstride(v, 2);
@@ -137,8 +181,37 @@ extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k,
   p.nblocks = B * Hkv * a.nkb;
   // one work-group per image (grid x dimension), 32-bit indexed in the kernel
   if (p.nblocks > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "K/V too large");
+  if (Tq == 0) return SIA_OK;
   L.D = (int)D;
   L.dtype = q->dtype;
   L.stream = (hipStream_t)stream;
   return launch_prefill(L);
+}
+
+}  // namespace
+
+extern "C" int sia_prefill_workspace_size(int64_t batch, int64_t kv_heads, int64_t kv_len, int64_t head_dim,
+                                          size_t* bytes) {
+  if (bytes == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "bytes is NULL");
+  if (batch <= 0 || kv_heads <= 0 || kv_len < 0) return fail(SIA_ERR_INVALID_ARGUMENT, "bad sizes");
+  if (!head_dim_ok(head_dim))
+    return fail(SIA_ERR_UNSUPPORTED, "prefill head_dim %lld not supported (16, 32, 64, 128, 256)",
+                (long long)head_dim);
+  *bytes = (size_t)image_bytes(batch, kv_heads, kv_len, head_dim);
+  return SIA_OK;
+}
+
+extern "C" int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
+                                       float sm_scale, const sia_tensor* out, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  return flash_fwd(q, k, v, causal, sm_scale, out, workspace, workspace_bytes, stream, nullptr);
+}
+
+extern "C" int sia_attention_flash_fwd_rope(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v,
+                                            const sia_tensor* cos, const sia_tensor* sin, int32_t interleaved,
+                                            const sia_tensor* start_pos, int32_t start_pos_host, int32_t causal,
+                                            float sm_scale, const sia_tensor* out, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  const RopeIn r{cos, sin, start_pos, start_pos_host, interleaved};
+  return flash_fwd(q, k, v, causal, sm_scale, out, workspace, workspace_bytes, stream, &r);
 }

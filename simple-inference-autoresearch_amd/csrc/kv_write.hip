@@ -110,12 +110,6 @@ template <class S> __device__ __forceinline__ float to_src(float x) { return x; 
 template <> __device__ __forceinline__ float to_src<F16>(float x) { return (float)(_Float16)x; }
 template <> __device__ __forceinline__ float to_src<BF16>(float x) { return (float)(__bf16)x; }
 
-__device__ __forceinline__ void rot(float xa, float xb, float c, float s, float& oa, float& ob) {
-#pragma clang fp contract(off)
-  oa = xa * c - xb * s;
-  ob = xb * c + xa * s;
-}
-
 // Rotate this lane's 8 elements of a K row (lane `part` of the row's `width`
 // lanes holds elements [8 part, 8 part + 8)) by table row `pos` (already
 // clamped into the table).  Split-half: the partner elements sit in lane
@@ -139,15 +133,15 @@ __device__ __forceinline__ void rope8(float (&x)[8], int part, int width, const 
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float oa, ob;
-      if (first) rot(x[i], y[i], c[i], s[i], oa, ob);
-      else rot(y[i], x[i], c[i], s[i], ob, oa);
+      if (first) rope_rotate(x[i], y[i], c[i], s[i], oa, ob);
+      else rope_rotate(y[i], x[i], c[i], s[i], ob, oa);
       x[i] = oa;
     }
   } else {
     tab_n<C, 4>(crow, part * 4, c);
     tab_n<C, 4>(srow, part * 4, s);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) rot(x[2 * j], x[2 * j + 1], c[j], s[j], x[2 * j], x[2 * j + 1]);
+    for (int j = 0; j < 4; ++j) rope_rotate(x[2 * j], x[2 * j + 1], c[j], s[j], x[2 * j], x[2 * j + 1]);
   }
 }
 
@@ -211,12 +205,12 @@ __device__ __forceinline__ void rope_q_token(const KvWriteArgs& a, uint32_t toke
     }
     if constexpr (ROPE == 1) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) rot(x0[i], x1[i], c[i], s[i], x0[i], x1[i]);
+      for (int i = 0; i < 8; ++i) rope_rotate(x0[i], x1[i], c[i], s[i], x0[i], x1[i]);
     } else {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) rot(x0[2 * j], x0[2 * j + 1], c[j], s[j], x0[2 * j], x0[2 * j + 1]);
+      for (int j = 0; j < 4; ++j) rope_rotate(x0[2 * j], x0[2 * j + 1], c[j], s[j], x0[2 * j], x0[2 * j + 1]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) rot(x1[2 * j], x1[2 * j + 1], c[4 + j], s[4 + j], x1[2 * j], x1[2 * j + 1]);
+      for (int j = 0; j < 4; ++j) rope_rotate(x1[2 * j], x1[2 * j + 1], c[4 + j], s[4 + j], x1[2 * j], x1[2 * j + 1]);
     }
     store8<S>(dst + o0 * ES, x0);
     store8<S>(dst + o1 * ES, x1);

@@ -7,12 +7,16 @@ namespace sia {
 
 template <int D, class T>
 static int launch_prefill_typed(PrefillLaunch& L) {
+  const bool rope = L.a.cs != nullptr;
   if (L.pack.nblocks > 0) {
     // one work-group per 64-key V^T image
     hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)L.pack.nblocks), dim3(256), 0, L.stream, L.pack);
   }
   const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
-  hipLaunchKernelGGL((prefill_fwd<D, T>), dim3(nwg), dim3(PfCfg<D>::waves * 64), 0, L.stream, L.a);
+  if (rope)
+    hipLaunchKernelGGL((prefill_fwd<D, T, true>), dim3(nwg), dim3(PfCfg<D>::waves * 64), 0, L.stream, L.a);
+  else
+    hipLaunchKernelGGL((prefill_fwd<D, T, false>), dim3(nwg), dim3(PfCfg<D>::waves * 64), 0, L.stream, L.a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
   return SIA_OK;

@@ -63,6 +63,13 @@ struct PrefillArgs {
   int32_t nqblk;                                // ceil(Tq / 128)
   int32_t nkb;                                  // ceil(Tk / 64)
   int32_t remap;                                // XCD-aware block order
+  // rotary embedding of q at load (prefill_fwd<D, T, true> only): query row
+  // i of sequence b sits at position start_host + start_pos[b or 0] + i
+  // (start_pos NULL: 0) and is rotated by row pos of the cos/sin tables
+  // (first D/2 columns; a position outside the table rotates to zeros)
+  const char* cs; const char* sn; int64_t tab_rs;
+  int32_t Tc, tab_dt, interleaved;
+  const int32_t* start_pos; int32_t start_host, pos_per_seq;
 };
 
 struct PackArgs {
@@ -165,6 +172,106 @@ __global__ __launch_bounds__(256) void prefill_pack_v(const PackArgs a) {
   }
 }
 
+// n consecutive table entries (n = 4 or 8) of a cos/sin row as fp32; the
+// table dtype is a runtime value (read once per work-group)
+template <int N>
+__device__ __forceinline__ void tab_load(const char* p, int dt, float* x) {
+  if (dt == SIA_F32) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const f32x4 v = *(const f32x4*)(p + 16 * i);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[4 * i + e] = v[e];
+    }
+  } else {
+    uint32_t w[N / 2];
+    if constexpr (N == 8) {
+      const u32x4 v = *(const u32x4*)p;
+      w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+    } else {
+      const u32x2 v = *(const u32x2*)p;
+      w[0] = v[0]; w[1] = v[1];
+    }
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      x[2 * i] = dt == SIA_BF16 ? lo_f32(BF16{}, w[i]) : lo_f32(F16{}, w[i]);
+      x[2 * i + 1] = dt == SIA_BF16 ? hi_f32(BF16{}, w[i]) : hi_f32(F16{}, w[i]);
+    }
+  }
+}
+
+// Rotate this lane's Q operand in registers: qop[j] holds q[d] for
+// d = 16 j + 8 h + [0, 8) of the query at position pos.  Split-half pairs
+// (d, d + D/2) sit in qop[j] and qop[j + D/32] of the same lane (for D = 16,
+// in the lanes l and l ^ 32); interleaved pairs (2i, 2i + 1) sit in one
+// word.  The arithmetic is rope_rotate's, then a round to T: the same bits as
+// the rotation kernels produce.
+template <int D, class T>
+__device__ __forceinline__ void rope_q_operand(const PrefillArgs& a, u32x4* qop, int64_t pos, int h) {
+  constexpr int KST = D / 16;
+  const bool ok = pos >= 0 && pos < a.Tc;
+  const int64_t ro = (int64_t)(ok ? pos : 0) * a.tab_rs;
+  const char* crow = a.cs + ro;
+  const char* srow = a.sn + ro;
+  const int es = a.tab_dt == SIA_F32 ? 4 : 2;
+  if (a.interleaved) {
+#pragma unroll
+    for (int j = 0; j < KST; ++j) {
+      float c[4], sn[4];
+      const int i0 = 8 * j + 4 * h;                       // first pair of the 8 elements
+      tab_load<4>(crow + i0 * es, a.tab_dt, c);
+      tab_load<4>(srow + i0 * es, a.tab_dt, sn);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        float y0, y1;
+        rope_rotate(lo_f32(T{}, qop[j][w]), hi_f32(T{}, qop[j][w]), c[w], sn[w], y0, y1);
+        qop[j][w] = ok ? pack2(T{}, y0, y1) : 0u;
+      }
+    }
+  } else if constexpr (KST >= 2) {
+#pragma unroll
+    for (int j = 0; j < KST / 2; ++j) {
+      float c[8], sn[8];
+      const int i0 = 16 * j + 8 * h;
+      tab_load<8>(crow + i0 * es, a.tab_dt, c);
+      tab_load<8>(srow + i0 * es, a.tab_dt, sn);
+      u32x4& xa = qop[j];
+      u32x4& xb = qop[j + KST / 2];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        float a0, b0, a1, b1;
+        rope_rotate(lo_f32(T{}, xa[w]), lo_f32(T{}, xb[w]), c[2 * w], sn[2 * w], a0, b0);
+        rope_rotate(hi_f32(T{}, xa[w]), hi_f32(T{}, xb[w]), c[2 * w + 1], sn[2 * w + 1], a1, b1);
+        xa[w] = ok ? pack2(T{}, a0, a1) : 0u;
+        xb[w] = ok ? pack2(T{}, b0, b1) : 0u;
+      }
+    }
+  } else {
+    // D = 16: dims 0-7 in lanes 0-31, their partners 8-15 in lanes 32-63
+    float c[8], sn[8];
+    tab_load<8>(crow, a.tab_dt, c);
+    tab_load<8>(srow, a.tab_dt, sn);
+    u32x4 other;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const auto r = __builtin_amdgcn_permlane32_swap(qop[0][w], qop[0][w], false, false);
+      other[w] = h ? (uint32_t)r[0] : (uint32_t)r[1];
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      float o0, o1, t0, t1;
+      if (h == 0) {
+        rope_rotate(lo_f32(T{}, qop[0][w]), lo_f32(T{}, other[w]), c[2 * w], sn[2 * w], o0, t0);
+        rope_rotate(hi_f32(T{}, qop[0][w]), hi_f32(T{}, other[w]), c[2 * w + 1], sn[2 * w + 1], o1, t1);
+      } else {
+        rope_rotate(lo_f32(T{}, other[w]), lo_f32(T{}, qop[0][w]), c[2 * w], sn[2 * w], t0, o0);
+        rope_rotate(hi_f32(T{}, other[w]), hi_f32(T{}, qop[0][w]), c[2 * w + 1], sn[2 * w + 1], t1, o1);
+      }
+      qop[0][w] = ok ? pack2(T{}, o0, o1) : 0u;
+    }
+  }
+}
+
 template <int P>
 struct PfParity {
   static constexpr int value = P;
@@ -207,7 +314,7 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
   }
 }
 
-template <int D, class T>
+template <int D, class T, bool ROPE>
 __global__ __launch_bounds__(PfCfg<D>::waves * 64) __attribute__((amdgpu_waves_per_eu(PfCfg<D>::wpe)))
 void prefill_fwd(const PrefillArgs a) {
   using C = PfCfg<D>;
@@ -261,6 +368,10 @@ void prefill_fwd(const PrefillArgs a) {
     const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)min(qi, a.Tq - 1) * a.q_sm + 16 * h;
 #pragma unroll
     for (int j = 0; j < KST; ++j) qop[j] = qi < a.Tq ? *(const u32x4*)(qp + 32 * j) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (ROPE) {
+      const int64_t base = (int64_t)a.start_host + (a.start_pos != nullptr ? a.start_pos[a.pos_per_seq ? b : 0] : 0);
+      rope_q_operand<D, T>(a, qop, base + qi, h);
+    }
   }
 
   const int kend = a.causal ? min(a.Tk, off + q0 + BM) : a.Tk;

@@ -78,15 +78,6 @@ __device__ __forceinline__ void st8(char* p, const float* x) {
   }
 }
 
-// Products and sums rounded one by one: hipcc contracts a*b - c*d into an FMA
-// by default (and __fmul_rn is a plain multiply in this toolchain), so the
-// contraction is switched off for this block.
-__device__ __forceinline__ void rotate(float xa, float xb, float c, float s, float& oa, float& ob) {
-#pragma clang fp contract(off)
-  oa = xa * c - xb * s;
-  ob = xb * c + xa * s;
-}
-
 // VEC: 8 pairs per work item (16-byte accesses); otherwise one pair.
 template <class T, class C, bool IL, bool VEC>
 __global__ __launch_bounds__(1024) void rope_qk_kernel(const RopeArgs a) {
@@ -124,7 +115,7 @@ __global__ __launch_bounds__(1024) void rope_qk_kernel(const RopeArgs a) {
         x[1] = ld1<T>(src + (2 * i0 + 1) * ES);
       }
 #pragma unroll
-      for (int p = 0; p < PP; ++p) rotate(x[2 * p], x[2 * p + 1], c[p], s[p], o[2 * p], o[2 * p + 1]);
+      for (int p = 0; p < PP; ++p) rope_rotate(x[2 * p], x[2 * p + 1], c[p], s[p], o[2 * p], o[2 * p + 1]);
       if constexpr (VEC) {
         st8<T>(dst + 2 * i0 * ES, o);
         st8<T>(dst + (2 * i0 + 8) * ES, o + 8);
@@ -143,7 +134,7 @@ __global__ __launch_bounds__(1024) void rope_qk_kernel(const RopeArgs a) {
         xb[0] = ld1<T>(src + (i0 + half) * ES);
       }
 #pragma unroll
-      for (int p = 0; p < PP; ++p) rotate(xa[p], xb[p], c[p], s[p], oa[p], ob[p]);
+      for (int p = 0; p < PP; ++p) rope_rotate(xa[p], xb[p], c[p], s[p], oa[p], ob[p]);
       if constexpr (VEC) {
         st8<T>(dst + i0 * ES, oa);
         st8<T>(dst + (i0 + half) * ES, ob);

@@ -133,6 +133,17 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// One rotary-embedding pair: oa = xa c - xb s, ob = xb c + xa s in fp32 with
+// every product and sum rounded on its own.  hipcc contracts a*b - c*d into
+// an FMA by default (and __fmul_rn is a plain multiply in this toolchain), so
+// the contraction is switched off here: the result is a fixed function of
+// the inputs, shared by every kernel that rotates q or k.
+__device__ __forceinline__ void rope_rotate(float xa, float xb, float c, float s, float& oa, float& ob) {
+#pragma clang fp contract(off)
+  oa = xa * c - xb * s;
+  ob = xb * c + xa * s;
+}
+
 // ------------------------------------------------------------------- loads
 
 template <int BYTES>

@@ -66,3 +66,37 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
         return out if out_token_major else out.view(B, Hq, 1, D)
     q, k, v = (t if _supported_view(t) else t.contiguous() for t in (q, k, v))
     return ops.prefill(q, k, v, bool(causal), float(sm_scale), bool(out_token_major))
+
+
+def rope_attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                                sin: torch.Tensor, causal: bool, sm_scale: float | None = None,
+                                start_pos: torch.Tensor | None = None, start_offset: int = 0,
+                                interleaved: bool = False, out_token_major: bool = False) -> torch.Tensor:
+    """``attention_flash_triton(rope(q), k, v)`` in one launch (``sia_attention_flash_fwd_rope``).
+
+    The pair the reference's prefill runs -- ``apply_rope`` on q
+    (``ops/attention.py:291-292``, ``kernels/rope_kernel.py:261``) then
+    ``attention_flash_triton`` (``ops/attention.py:327-330``) -- with q rotated
+    in registers as it is loaded, so no rotated copy of q is written or read.
+    ``q (B, Hq, Tq, D)`` is un-rotated; ``k`` already holds rotated keys
+    (e.g. the cache that :func:`rope_kv_write` with ``q=None`` filled).  Query
+    row ``i`` of sequence ``b`` sits at position
+    ``start_offset + start_pos[b] + i`` (``start_pos``: int32 device tensor of
+    1 or B elements, or None for 0) and is rotated by that row of the full
+    ``cos``/``sin`` tables.  The rotation is :func:`rope_triton`'s arithmetic
+    and rounding, so the result equals ``rope_triton`` then
+    ``attention_flash_triton`` bit for bit.  float16/bfloat16 only.
+    """
+    B, Hq, Tq, D = q.shape
+    if not (k.shape[-1] == D and v.shape[-1] == D):
+        raise AssertionError()
+    if D not in _HEAD_DIMS:
+        raise AssertionError(f"unsupported head_dim {D}")
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise NotImplementedError("the fused rotary prologue runs on float16/bfloat16 inputs; "
+                                  "use rope_triton then attention_flash_triton for float32")
+    if sm_scale is None:
+        sm_scale = 1.0 / (D ** 0.5)
+    q, k, v = (t if _supported_view(t) else t.contiguous() for t in (q, k, v))
+    return _lib.gpu_ops().prefill_rope(q, k, v, cos, sin, bool(interleaved), start_pos, int(start_offset),
+                                       bool(causal), float(sm_scale), bool(out_token_major))

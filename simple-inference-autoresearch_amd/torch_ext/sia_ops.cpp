@@ -189,6 +189,30 @@ Tensor prefill(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, d
   return out;
 }
 
+// prefill with q rotated at load: q (B, Hq, Tq, D) un-rotated, k rotated.
+Tensor prefill_rope(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& cos, const Tensor& sin,
+                    bool interleaved, const OptT& start_pos, int64_t start_offset, bool causal, double sm_scale,
+                    bool out_token_major) {
+  const at::Device dev = gpu_of(q, "q");
+  const c10::DeviceGuard guard(dev);
+  if (q.dim() != 4 || k.dim() != 4) throw py::value_error("q, k and v must have 4 dims");
+  const int64_t B = q.size(0), Hq = q.size(1), Tq = q.size(2), D = q.size(3);
+  const int64_t Hkv = k.size(1), Tk = k.size(2);
+  const sia_tensor dq = desc(q, dev, "q"), dk = desc(k, dev, "k"), dv = desc(v, dev, "v"),
+                   dc = desc(cos, dev, "cos"), dsn = desc(sin, dev, "sin");
+  const OptDesc dsp(start_pos, dev, "start_pos");
+  Tensor out = out_token_major ? at::empty({B, Tq, Hq, D}, q.options()) : at::empty({B, Hq, Tq, D}, q.options());
+  const Tensor view = out_token_major ? out.transpose(1, 2) : out;
+  const sia_tensor dout = desc(view, dev, "out");
+  size_t ws_bytes = 0;
+  if (q.scalar_type() != at::kFloat) check(sia_prefill_workspace_size(B, Hkv, Tk, D, &ws_bytes));
+  Tensor ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
+  check(sia_attention_flash_fwd_rope(&dq, &dk, &dv, &dc, &dsn, interleaved ? 1 : 0, dsp.ptr(), (int32_t)start_offset,
+                                     causal ? 1 : 0, (float)sm_scale, &dout, ws.data_ptr(), ws_bytes,
+                                     stream_of(dev)));
+  return out;
+}
+
 std::tuple<Tensor, Tensor> quantize_kv_int8(const Tensor& x, bool scale_f32) {
   const at::Device dev = gpu_of(x, "x");
   const c10::DeviceGuard guard(dev);
@@ -268,6 +292,7 @@ PYBIND11_MODULE(_sia_ops, m) {
   });
   m.def("decode", &decode);
   m.def("prefill", &prefill);
+  m.def("prefill_rope", &prefill_rope);
   m.def("quantize_kv_int8", &quantize_kv_int8);
   m.def("kv_write", &kv_write);
   m.def("rope_kv_write", &rope_kv_write);

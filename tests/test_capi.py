@@ -95,7 +95,7 @@ def test_torch_extension_loads_and_binds_the_library(lib):
     lib_mod = import_module("simple-inference-autoresearch_amd._lib")
     ops = lib_mod.ops()
     assert ops.abi_version() == lib.sia_abi_version() == 1
-    for name in ("decode", "prefill", "quantize_kv_int8", "kv_write", "rope_kv_write", "rope_qk",
+    for name in ("decode", "prefill", "prefill_rope", "quantize_kv_int8", "kv_write", "rope_kv_write", "rope_qk",
                  "decode_workspace_size", "prefill_workspace_size"):
         assert callable(getattr(ops, name)), name
     n = ctypes.c_size_t(0)
