@@ -239,7 +239,31 @@ def bench_prefill_config(pkg, steps: int, warmup: int):
     tf = flops / (ms * 1e-3) / 1e12
     return {**_timing_fields(t), "TFLOPs": round(tf, 1), "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
             "algorithmic_flops": flops, "workload": "config 4: causal prefill bf16 B4 T2048 32/8 heads D128",
-            "statistic": f"median of {steps} calls"}
+            "statistic": f"median of {steps} calls",
+            "rope_prologue": bench_rope_prologue(pkg, q, k, v, steps, warmup)}
+
+
+def bench_rope_prologue(pkg, q, k, v, steps: int, warmup: int):
+    """The same prefill with q rotated as it is loaded (rope_attention_flash_triton) against
+    the reference's order for q: rope_triton, then attention on the rotated copy.  q is
+    token-major (B, T, Hq, D), as the qkv projection leaves it, so both read it in place;
+    K is taken as already rotated in both (the cache write rotates it)."""
+    B, Hq, T, D = q.shape
+    rf = pkg.RopeFrequencies(D, T, device=q.device)
+    cos, sin = rf.get(T, start_pos=0, dtype=q.dtype)
+    q_tm = q.transpose(1, 2).contiguous()
+    k1 = q_tm[:, :, :1]        # rope_triton rotates a k as well: one head, negligible
+
+    def unfused():
+        qr, _ = pkg.rope_triton(q_tm, k1, cos, sin)
+        return pkg.attention_flash_triton(qr.transpose(1, 2), k, v, causal=True, out_token_major=True)
+
+    fused = time_calls(lambda: pkg.rope_attention_flash_triton(q_tm.transpose(1, 2), k, v, cos, sin, causal=True,
+                                                                out_token_major=True), steps, warmup)
+    sep = time_calls(unfused, steps, warmup)
+    return {"fused_us_per_call": round(fused["median_ms"] * 1e3, 2),
+            "rope_then_attention_us_per_call": round(sep["median_ms"] * 1e3, 2),
+            "statistic": f"median of {steps} calls each"}
 
 
 def bench_config1(pkg, steps: int, warmup: int):

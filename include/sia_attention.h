@@ -182,7 +182,8 @@ int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_
  * per sequence, read on the device) or NULL (p = start_pos_host + i, checked
  * against the table rows on the host: SIA_ERR_INVALID_ARGUMENT).  cos, sin
  * as for sia_rope_qk (row p of the table, first D/2 columns, 16-byte aligned
- * rows); interleaved 0: pairs (i, i + D/2), 1: pairs (2i, 2i + 1).  The
+ * rows) but in q's dtype or float32 (another dtype: SIA_ERR_UNSUPPORTED);
+ * interleaved 0: pairs (i, i + D/2), 1: pairs (2i, 2i + 1).  The
  * rotation is sia_rope_qk's arithmetic and rounding, so the result equals
  * sia_rope_qk followed by sia_attention_flash_fwd bit for bit.  A device
  * position outside the table rotates q to zeros.  float16/bfloat16 only

@@ -74,7 +74,7 @@ struct RopeIn {
 
 // Checks the tables and positions against q (B, Hq, Tq, D) and fills the
 // rotation fields of the kernel arguments.
-int setup_rope(const RopeIn& r, int64_t B, int64_t Tq, int64_t D, PrefillArgs& a) {
+int setup_rope(const RopeIn& r, int64_t B, int64_t Tq, int64_t D, int q_dtype, PrefillArgs& a) {
   const sia_tensor* cos = r.cos;
   const sia_tensor* sin = r.sin;
   if (cos == nullptr || sin == nullptr || cos->data == nullptr || sin->data == nullptr || cos->ndim != 2 ||
@@ -87,6 +87,9 @@ int setup_rope(const RopeIn& r, int64_t B, int64_t Tq, int64_t D, PrefillArgs& a
                 (long long)D, (long long)(D / 2));
   if (cos->dtype != sin->dtype || (cos->dtype != SIA_F16 && cos->dtype != SIA_BF16 && cos->dtype != SIA_F32))
     return fail(SIA_ERR_INVALID_ARGUMENT, "cos and sin must share a float dtype");
+  if (cos->dtype != q_dtype && cos->dtype != SIA_F32)
+    return fail(SIA_ERR_UNSUPPORTED, "cos/sin dtype %s: the fused prologue reads tables in q's dtype or float32",
+                dtype_name(cos->dtype));
   if (cos->stride[1] != 1 || sin->stride[1] != 1 || cos->stride[0] != sin->stride[0])
     return fail(SIA_ERR_INVALID_ARGUMENT, "cos/sin must be unit-stride rows with one row stride");
   if (cos->shape[0] <= 0 || cos->shape[0] > 0x7fffffff) return fail(SIA_ERR_INVALID_ARGUMENT, "bad table row count");
@@ -172,7 +175,7 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   const int64_t groups = (int64_t)a.nqblk * B * Hkv;   // work-groups come in runs of G sharing a KV head
   if (groups * a.G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "grid too large");
   a.remap = groups % 8 == 0;
-  if (rope != nullptr && (rc = setup_rope(*rope, B, Tq, D, a))) return rc;
+  if (rope != nullptr && (rc = setup_rope(*rope, B, Tq, D, q->dtype, a))) return rc;
 
   PackArgs& p = L.pack;
   p.v = (const char*)v->data; p.v_sb = bstride(v, 0); p.v_sh = bstride(v, 1); p.v_sn = bstride(v, 2);

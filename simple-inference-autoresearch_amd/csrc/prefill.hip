@@ -7,16 +7,21 @@ namespace sia {
 
 template <int D, class T>
 static int launch_prefill_typed(PrefillLaunch& L) {
-  const bool rope = L.a.cs != nullptr;
+  // rotary variant: none, or split-half / interleaved pairs from 16-bit / fp32 tables
+  const int rope = L.a.cs == nullptr ? kRopeNone : 1 + (L.a.interleaved ? 1 : 0) + (L.a.tab_dt == SIA_F32 ? 2 : 0);
   if (L.pack.nblocks > 0) {
     // one work-group per 64-key V^T image
     hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)L.pack.nblocks), dim3(256), 0, L.stream, L.pack);
   }
   const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
-  if (rope)
-    hipLaunchKernelGGL((prefill_fwd<D, T, true>), dim3(nwg), dim3(PfCfg<D>::waves * 64), 0, L.stream, L.a);
-  else
-    hipLaunchKernelGGL((prefill_fwd<D, T, false>), dim3(nwg), dim3(PfCfg<D>::waves * 64), 0, L.stream, L.a);
+  const dim3 grid(nwg), block(PfCfg<D>::waves * 64);
+  switch (rope) {
+    case kRopeNone: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeNone>), grid, block, 0, L.stream, L.a); break;
+    case kRopeSplit16: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeSplit16>), grid, block, 0, L.stream, L.a); break;
+    case kRopeInter16: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeInter16>), grid, block, 0, L.stream, L.a); break;
+    case kRopeSplit32: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeSplit32>), grid, block, 0, L.stream, L.a); break;
+    default: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeInter32>), grid, block, 0, L.stream, L.a); break;
+  }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
   return SIA_OK;

@@ -172,69 +172,108 @@ __global__ __launch_bounds__(256) void prefill_pack_v(const PackArgs a) {
   }
 }
 
-// n consecutive table entries (n = 4 or 8) of a cos/sin row as fp32; the
-// table dtype is a runtime value (read once per work-group)
-template <int N>
-__device__ __forceinline__ void tab_load(const char* p, int dt, float* x) {
-  if (dt == SIA_F32) {
+// Rotary prologue variants of prefill_fwd: q rotated as it is loaded, with
+// split-half pairs (i, i + D/2) or interleaved pairs (2i, 2i + 1), from
+// cos/sin tables in q's dtype or in fp32.
+enum : int { kRopeNone = 0, kRopeSplit16 = 1, kRopeInter16 = 2, kRopeSplit32 = 3, kRopeInter32 = 4 };
+
+// The cos/sin entries one lane needs to rotate its Q operand (qop[j] holds
+// q[d], d = 16 j + 8 h + [0, 8)): split-half pairs (d, d + D/2) use columns
+// 16 j + 8 h + [0, 8) for j < D/32 (D = 16: columns 0-7 in both half-waves);
+// interleaved pairs (2i, 2i + 1) use columns 8 j + 4 h + [0, 4) for j < D/16.
+// They are fetched into registers together with q, before the first K/V
+// transfers are issued, and used once those are in flight: every variant
+// issues a fixed number of loads, so the wait before the rotation covers q
+// and the tables alone.
+template <int D, int ROPE>
+struct RopeQ {
+  static constexpr int EW = ROPE >= kRopeSplit32 ? 2 : 1;             // words per two entries
+  static constexpr int NW = (D / 8 > 4 ? D / 8 : 4) * EW;             // words per table
+  uint32_t c[ROPE ? NW : 1], s[ROPE ? NW : 1];
+  bool ok;                                                           // the position has a table row
+};
+
+template <int D, int ROPE>
+__device__ __forceinline__ void rope_q_fetch(const PrefillArgs& a, RopeQ<D, ROPE>& r, int64_t pos, int h) {
+  constexpr int KST = D / 16;
+  constexpr int ES = ROPE >= kRopeSplit32 ? 4 : 2;                    // table entry bytes
+  r.ok = pos >= 0 && pos < a.Tc;
+  const int64_t ro = (int64_t)(r.ok ? pos : 0) * a.tab_rs;
+  const char* crow = a.cs + ro;
+  const char* srow = a.sn + ro;
+  // n 16-byte or 8-byte pieces from column col of both rows into words w0..
+  auto take = [&](int col, int w0, int bytes) {
 #pragma unroll
-    for (int i = 0; i < N / 4; ++i) {
-      const f32x4 v = *(const f32x4*)(p + 16 * i);
+    for (int off = 0; off < bytes; off += 16) {
+      if (bytes - off >= 16) {
+        const u32x4 cv = *(const u32x4*)(crow + ES * col + off), sv = *(const u32x4*)(srow + ES * col + off);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) x[4 * i + e] = v[e];
+        for (int e = 0; e < 4; ++e) {
+          r.c[w0 + off / 4 + e] = cv[e];
+          r.s[w0 + off / 4 + e] = sv[e];
+        }
+      } else {
+        const u32x2 cv = *(const u32x2*)(crow + ES * col + off), sv = *(const u32x2*)(srow + ES * col + off);
+        r.c[w0 + off / 4] = cv[0]; r.c[w0 + off / 4 + 1] = cv[1];
+        r.s[w0 + off / 4] = sv[0]; r.s[w0 + off / 4 + 1] = sv[1];
+      }
     }
+  };
+  if constexpr (ROPE == kRopeInter16 || ROPE == kRopeInter32) {
+#pragma unroll
+    for (int j = 0; j < KST; ++j) take(8 * j + 4 * h, 2 * RopeQ<D, ROPE>::EW * j, 4 * ES);
   } else {
-    uint32_t w[N / 2];
-    if constexpr (N == 8) {
-      const u32x4 v = *(const u32x4*)p;
-      w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
-    } else {
-      const u32x2 v = *(const u32x2*)p;
-      w[0] = v[0]; w[1] = v[1];
-    }
+    constexpr int NQ = KST >= 2 ? KST / 2 : 1;
 #pragma unroll
-    for (int i = 0; i < N / 2; ++i) {
-      x[2 * i] = dt == SIA_BF16 ? lo_f32(BF16{}, w[i]) : lo_f32(F16{}, w[i]);
-      x[2 * i + 1] = dt == SIA_BF16 ? hi_f32(BF16{}, w[i]) : hi_f32(F16{}, w[i]);
+    for (int j = 0; j < NQ; ++j) take(KST >= 2 ? 16 * j + 8 * h : 0, 4 * RopeQ<D, ROPE>::EW * j, 8 * ES);
+  }
+}
+
+// N consecutive entries from fetched words w (16-bit tables hold q's dtype T)
+template <int N, bool F32T, class T>
+__device__ __forceinline__ void tab_vals(const uint32_t* w, float* x) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    if constexpr (F32T) {
+      x[2 * i] = __builtin_bit_cast(float, w[2 * i]);
+      x[2 * i + 1] = __builtin_bit_cast(float, w[2 * i + 1]);
+    } else {
+      x[2 * i] = lo_f32(T{}, w[i]);
+      x[2 * i + 1] = hi_f32(T{}, w[i]);
     }
   }
 }
 
-// Rotate this lane's Q operand in registers: qop[j] holds q[d] for
-// d = 16 j + 8 h + [0, 8) of the query at position pos.  Split-half pairs
-// (d, d + D/2) sit in qop[j] and qop[j + D/32] of the same lane (for D = 16,
-// in the lanes l and l ^ 32); interleaved pairs (2i, 2i + 1) sit in one
-// word.  The arithmetic is rope_rotate's, then a round to T: the same bits as
-// the rotation kernels produce.
-template <int D, class T>
-__device__ __forceinline__ void rope_q_operand(const PrefillArgs& a, u32x4* qop, int64_t pos, int h) {
+// Rotate this lane's Q operand in registers.  Split-half pairs sit in qop[j]
+// and qop[j + D/32] of the same lane (for D = 16, in the lanes l and l ^ 32);
+// interleaved pairs sit in one word.  The arithmetic is rope_rotate's, then
+// a round to T: the same bits as the rotation kernels produce.  A position
+// without a table row rotates q to zeros.
+template <int D, class T, int ROPE>
+__device__ __forceinline__ void rope_q_apply(const PrefillArgs& a, u32x4* qop, const RopeQ<D, ROPE>& r, int h) {
   constexpr int KST = D / 16;
-  const bool ok = pos >= 0 && pos < a.Tc;
-  const int64_t ro = (int64_t)(ok ? pos : 0) * a.tab_rs;
-  const char* crow = a.cs + ro;
-  const char* srow = a.sn + ro;
-  const int es = a.tab_dt == SIA_F32 ? 4 : 2;
-  if (a.interleaved) {
+  constexpr bool F32T = ROPE >= kRopeSplit32;
+  constexpr int EW = RopeQ<D, ROPE>::EW;
+  const uint32_t ok = r.ok ? 0xffffffffu : 0u;   // a mask, not a branch around the rotation
+  if constexpr (ROPE == kRopeInter16 || ROPE == kRopeInter32) {
 #pragma unroll
     for (int j = 0; j < KST; ++j) {
       float c[4], sn[4];
-      const int i0 = 8 * j + 4 * h;                       // first pair of the 8 elements
-      tab_load<4>(crow + i0 * es, a.tab_dt, c);
-      tab_load<4>(srow + i0 * es, a.tab_dt, sn);
+      tab_vals<4, F32T, T>(r.c + 2 * EW * j, c);
+      tab_vals<4, F32T, T>(r.s + 2 * EW * j, sn);
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         float y0, y1;
         rope_rotate(lo_f32(T{}, qop[j][w]), hi_f32(T{}, qop[j][w]), c[w], sn[w], y0, y1);
-        qop[j][w] = ok ? pack2(T{}, y0, y1) : 0u;
+        qop[j][w] = pack2(T{}, y0, y1) & ok;
       }
     }
   } else if constexpr (KST >= 2) {
 #pragma unroll
     for (int j = 0; j < KST / 2; ++j) {
       float c[8], sn[8];
-      const int i0 = 16 * j + 8 * h;
-      tab_load<8>(crow + i0 * es, a.tab_dt, c);
-      tab_load<8>(srow + i0 * es, a.tab_dt, sn);
+      tab_vals<8, F32T, T>(r.c + 4 * EW * j, c);
+      tab_vals<8, F32T, T>(r.s + 4 * EW * j, sn);
       u32x4& xa = qop[j];
       u32x4& xb = qop[j + KST / 2];
 #pragma unroll
@@ -242,20 +281,20 @@ __device__ __forceinline__ void rope_q_operand(const PrefillArgs& a, u32x4* qop,
         float a0, b0, a1, b1;
         rope_rotate(lo_f32(T{}, xa[w]), lo_f32(T{}, xb[w]), c[2 * w], sn[2 * w], a0, b0);
         rope_rotate(hi_f32(T{}, xa[w]), hi_f32(T{}, xb[w]), c[2 * w + 1], sn[2 * w + 1], a1, b1);
-        xa[w] = ok ? pack2(T{}, a0, a1) : 0u;
-        xb[w] = ok ? pack2(T{}, b0, b1) : 0u;
+        xa[w] = pack2(T{}, a0, a1) & ok;
+        xb[w] = pack2(T{}, b0, b1) & ok;
       }
     }
   } else {
     // D = 16: dims 0-7 in lanes 0-31, their partners 8-15 in lanes 32-63
     float c[8], sn[8];
-    tab_load<8>(crow, a.tab_dt, c);
-    tab_load<8>(srow, a.tab_dt, sn);
+    tab_vals<8, F32T, T>(r.c, c);
+    tab_vals<8, F32T, T>(r.s, sn);
     u32x4 other;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const auto r = __builtin_amdgcn_permlane32_swap(qop[0][w], qop[0][w], false, false);
-      other[w] = h ? (uint32_t)r[0] : (uint32_t)r[1];
+      const auto x = __builtin_amdgcn_permlane32_swap(qop[0][w], qop[0][w], false, false);
+      other[w] = h ? (uint32_t)x[0] : (uint32_t)x[1];
     }
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -267,7 +306,7 @@ __device__ __forceinline__ void rope_q_operand(const PrefillArgs& a, u32x4* qop,
         rope_rotate(lo_f32(T{}, other[w]), lo_f32(T{}, qop[0][w]), c[2 * w], sn[2 * w], t0, o0);
         rope_rotate(hi_f32(T{}, other[w]), hi_f32(T{}, qop[0][w]), c[2 * w + 1], sn[2 * w + 1], t1, o1);
       }
-      qop[0][w] = ok ? pack2(T{}, o0, o1) : 0u;
+      qop[0][w] = pack2(T{}, o0, o1) & ok;
     }
   }
 }
@@ -314,7 +353,7 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
   }
 }
 
-template <int D, class T, bool ROPE>
+template <int D, class T, int ROPE>
 __global__ __launch_bounds__(PfCfg<D>::waves * 64) __attribute__((amdgpu_waves_per_eu(PfCfg<D>::wpe)))
 void prefill_fwd(const PrefillArgs a) {
   using C = PfCfg<D>;
@@ -364,13 +403,14 @@ void prefill_fwd(const PrefillArgs a) {
 
   // ---- Q^T operand (B of S^T = K Q^T): query qi, d = 16 j + 8 h + [0, 8)
   u32x4 qop[KST];
+  RopeQ<D, ROPE> rq;   // rotation inputs (applied once the first K/V transfers are issued)
   {
     const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)min(qi, a.Tq - 1) * a.q_sm + 16 * h;
 #pragma unroll
     for (int j = 0; j < KST; ++j) qop[j] = qi < a.Tq ? *(const u32x4*)(qp + 32 * j) : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (ROPE) {
+    if constexpr (ROPE != kRopeNone) {
       const int64_t base = (int64_t)a.start_host + (a.start_pos != nullptr ? a.start_pos[a.pos_per_seq ? b : 0] : 0);
-      rope_q_operand<D, T>(a, qop, base + qi, h);
+      rope_q_fetch<D, ROPE>(a, rq, base + qi, h);
     }
   }
 
@@ -608,6 +648,12 @@ void prefill_fwd(const PrefillArgs a) {
       issue_k(1, lk1);
       issue_k(2, lk2);
       issue_v(1, lv1);
+      if constexpr (ROPE != kRopeNone) {
+        // under the transfers' latency; nothing of the rotation (which waits
+        // for q) may be scheduled above the transfers
+        __builtin_amdgcn_sched_barrier(0);
+        rope_q_apply<D, T, ROPE>(a, qop, rq, h);
+      }
       wait_vmcnt(0);
       ring_barrier();
       first_scores();
@@ -634,6 +680,12 @@ void prefill_fwd(const PrefillArgs a) {
       issue_k(0, lk0);
       issue_v(0, lv0);
       issue_k(1, lk1);
+      if constexpr (ROPE != kRopeNone) {
+        // under the transfers' latency; nothing of the rotation (which waits
+        // for q) may be scheduled above the transfers
+        __builtin_amdgcn_sched_barrier(0);
+        rope_q_apply<D, T, ROPE>(a, qop, rq, h);
+      }
       wait_vmcnt(0);
       ring_barrier();
       first_scores();

@@ -97,6 +97,10 @@ def rope_attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
                                   "use rope_triton then attention_flash_triton for float32")
     if sm_scale is None:
         sm_scale = 1.0 / (D ** 0.5)
+    if cos.dtype not in (q.dtype, torch.float32) and cos.dtype in (torch.float16, torch.bfloat16):
+        # the kernel reads tables in q's dtype or fp32; widening the other
+        # 16-bit type to fp32 is exact, and the rotation runs in fp32 anyway
+        cos, sin = cos.float(), sin.float()
     q, k, v = (t if _supported_view(t) else t.contiguous() for t in (q, k, v))
     return _lib.gpu_ops().prefill_rope(q, k, v, cos, sin, bool(interleaved), start_pos, int(start_offset),
                                        bool(causal), float(sm_scale), bool(out_token_major))

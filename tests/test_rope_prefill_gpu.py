@@ -175,6 +175,23 @@ def test_kv_write_then_fused_prefill_pipeline(gpu_pkg):
     assert torch.equal(got, want)
 
 
+def test_tables_in_another_16_bit_dtype(gpu_pkg):
+    """bf16 q with f16 tables: the wrapper widens the tables to fp32 (exact), the result is unchanged."""
+    B, Hq, Hkv, T, D = 1, 8, 2, 90, 128
+    announce("rope prefill bf16 q, f16 tables")
+    q, k, v = inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=21)
+    cos, sin = tables(T, D, torch.float16)
+    got = gpu_pkg.rope_attention_flash_triton(q, k, v, cos, sin, causal=True)
+    want = unfused(gpu_pkg, q, k, v, cos, sin, [0], False, True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    from importlib import import_module
+    ops = import_module("simple-inference-autoresearch_amd._lib").gpu_ops()
+    with pytest.raises(NotImplementedError, match="dtype"):   # the C ABI itself takes q's dtype or fp32
+        ops.prefill_rope(q, k, v, cos, sin, False, None, 0, True, 0.1, False)
+    torch.cuda.synchronize()
+
+
 def test_argument_errors(gpu_pkg):
     q, k, v = inputs(1, 4, 1, 32, 32, 64, torch.bfloat16, seed=2)
     cos, sin = tables(40, 64, torch.bfloat16)
