@@ -600,13 +600,13 @@ void prefill_fwd(const PrefillArgs a) {
       for (int i = 0; i < 2 * KST; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one S MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // next operand read
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // softmax VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // softmax VALU
       }
 #pragma unroll
       for (int i = 0; i < 4 * ET; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one PV MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // softmax / row-max VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // softmax / row-max VALU
       }
       if (j + 1 >= wfull) {
         mask(sb0, sb1, (j + 1) * kPfBN);
@@ -698,11 +698,17 @@ void prefill_fwd(const PrefillArgs a) {
     if (j < nblk) step(PfParity<0>{}, j, s0, s1, n0, n1);
   }
 
-  // ---- normalise and store: lane owns query qi, d = 32 e + 8 (j / 4) + 4 h + j % 4
-  const float lt = half_swap_sum(l);
-  if (qi < a.Tq) {
+  // ---- normalise and store.  The lane owns query qi, d = 32 e + 8 (j / 4) +
+  // 4 h + j % 4 of O^T; the wave's 32 x D tile goes through LDS (16-byte
+  // chunks swizzled by row) so that every global store writes whole rows.
+  wait_vmcnt(0);                                         // every ring transfer (empty ones fill zeros) landed
+  ring_barrier();                                        // every wave is done with the ring
+  {
+    constexpr int NCH = D / 8;                           // 16-byte chunks per row
+    char* tile = (wave >> 1) == 0 ? lk0 : (wave >> 1) == 1 ? lk1 : (wave >> 1) == 2 ? lk2 : lk3;
+    tile += (wave & 1) * 32 * RB;
+    const float lt = half_swap_sum(l);
     const float inv = lt == 0.f ? 0.f : 1.0f / lt;
-    char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + (int64_t)qi * a.o_sm;
 #pragma unroll
     for (int e = 0; e < ET; ++e)
 #pragma unroll
@@ -711,8 +717,18 @@ void prefill_fwd(const PrefillArgs a) {
         u32x2 w;
         w[0] = pack2(T{}, o[e][4 * g4 + 0] * inv, o[e][4 * g4 + 1] * inv);
         w[1] = pack2(T{}, o[e][4 * g4 + 2] * inv, o[e][4 * g4 + 3] * inv);
-        *(u32x2*)(op + (32 * e + 8 * g4 + 4 * h) * 2) = w;
+        *(u32x2*)(tile + l32 * RB + (((4 * e + g4) ^ (l32 % NCH)) * 16) + h * 8) = w;
       }
+    constexpr int RPI = 64 / NCH;                        // rows per 64-lane pass
+    const int c = lane % NCH;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int row = i * RPI + lane / NCH;
+      const u32x4 w = *(const u32x4*)(tile + row * RB + ((c ^ (row % NCH)) * 16));
+      const int qrow = q0 + wave * 32 + row;
+      if (qrow < a.Tq)
+        *(u32x4*)(a.out + b * a.o_sb + (int64_t)hq * a.o_sh + (int64_t)qrow * a.o_sm + c * 16) = w;
+    }
   }
 }
 
