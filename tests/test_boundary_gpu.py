@@ -52,3 +52,10 @@ def test_prefill_and_writes_reject_host_tensors(gpu_pkg):
                             torch.randn(1, 4, 2, 128, device=DEV).to(torch.bfloat16), cos, cos)
     with pytest.raises(ValueError):
         gpu_pkg.quantize_kv_int8(torch.randn(4, 128))
+    with pytest.raises(ValueError):                                 # host rotary tables
+        gpu_pkg.rope_attention_flash_triton(q, k, k, torch.ones(64, 128, dtype=torch.bfloat16),
+                                            torch.ones(64, 128, dtype=torch.bfloat16), causal=True)
+    with pytest.raises(ValueError):                                 # host start positions
+        cg = torch.ones(64, 128, dtype=torch.bfloat16, device=DEV)
+        gpu_pkg.rope_attention_flash_triton(q, k, k, cg, cg, causal=True,
+                                            start_pos=torch.zeros(1, dtype=torch.int32))

@@ -192,6 +192,30 @@ def test_tables_in_another_16_bit_dtype(gpu_pkg):
     torch.cuda.synchronize()
 
 
+def test_graph_replays_at_new_device_positions(gpu_pkg):
+    """The fused prefill reads its positions on the device: one captured graph serves every
+    start position, and each replay equals the eager call."""
+    B, Hq, Hkv, T, D = 2, 8, 2, 96, 128
+    announce("rope prefill HIP-graph replay")
+    q, k, v = inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=31)
+    cos, sin = tables(512, D, torch.bfloat16)
+    sp = torch.tensor([0, 0], dtype=torch.int32, device=DEV)
+    gpu_pkg.rope_attention_flash_triton(q, k, v, cos, sin, causal=True, start_pos=sp)   # warm-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = gpu_pkg.rope_attention_flash_triton(q, k, v, cos, sin, causal=True, start_pos=sp)
+    for starts in ([0, 0], [5, 300], [17, 17], [400, 2]):
+        sp.copy_(torch.tensor(starts, dtype=torch.int32))
+        g.replay()
+        torch.cuda.synchronize()
+        want = gpu_pkg.rope_attention_flash_triton(q, k, v, cos, sin, causal=True,
+                                                   start_pos=torch.tensor(starts, dtype=torch.int32, device=DEV))
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), starts
+        assert torch.equal(want, unfused(gpu_pkg, q, k, v, cos, sin, starts, False, True)), starts
+
+
 def test_argument_errors(gpu_pkg):
     q, k, v = inputs(1, 4, 1, 32, 32, 64, torch.bfloat16, seed=2)
     cos, sin = tables(40, 64, torch.bfloat16)
