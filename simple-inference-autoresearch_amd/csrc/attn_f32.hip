@@ -301,6 +301,31 @@ static int launch_f32_d(F32Launch& L) {
   }
 }
 
+template <int D>
+static int launch_merge_d(const F32Args& a, int out_dtype, hipStream_t st) {
+  constexpr int RPB = 4 * (64 / (D / 4));
+  const int64_t rows = (int64_t)a.B * a.Hq * a.Tq;
+  const int64_t blocks = (rows + RPB - 1) / RPB;
+  if (blocks > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "split-K merge: too many rows");
+  if (blocks == 0) return SIA_OK;
+  if (out_dtype == SIA_F16) hipLaunchKernelGGL((attn_f32_merge<D, F16>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+  else if (out_dtype == SIA_BF16) hipLaunchKernelGGL((attn_f32_merge<D, BF16>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((attn_f32_merge<D, F32>), dim3((unsigned)blocks), dim3(256), 0, st, a);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? SIA_OK : fail(SIA_ERR_LAUNCH, "split-K merge launch: %s", hipGetErrorString(e));
+}
+
+int launch_attn_merge(const F32Args& a, int D, int out_dtype, hipStream_t stream) {
+  switch (D) {
+    case 16: return launch_merge_d<16>(a, out_dtype, stream);
+    case 32: return launch_merge_d<32>(a, out_dtype, stream);
+    case 64: return launch_merge_d<64>(a, out_dtype, stream);
+    case 128: return launch_merge_d<128>(a, out_dtype, stream);
+    case 256: return launch_merge_d<256>(a, out_dtype, stream);
+    default: return fail(SIA_ERR_UNSUPPORTED, "head_dim %d not supported (16, 32, 64, 128, 256)", D);
+  }
+}
+
 int launch_attn_f32(F32Launch& L) {
   if (L.q_dtype == SIA_F32) {
     switch (L.kv_dtype) {

@@ -70,6 +70,10 @@ struct F32Launch {
 // Launches attn_f32 (and attn_f32_merge when nsplit > 1); implemented in attn_f32.hip.
 int launch_attn_f32(F32Launch& L);
 
+// attn_f32_merge alone, for split-K partials written in its layout by another
+// kernel: head_dim D, output dtype out_dtype (f16 / bf16 / f32).
+int launch_attn_merge(const F32Args& a, int D, int out_dtype, hipStream_t stream);
+
 // Bytes of split-K partials for `rows` output rows, `nsplit` pieces, head_dim D.
 inline size_t f32_partial_bytes(int64_t rows, int64_t nsplit, int D) {
   return (size_t)rows * (size_t)nsplit * (size_t)(D + 4) * 4;

@@ -3,14 +3,22 @@
 //
 // The MFMA decode kernel (decode_kernel.hpp) tiles 16 tokens x head_dim with
 // at least four bytes per lane per token, which head_dim 16/32 cannot fill.
-// Here one wave serves one (sequence, query head): lanes stride over the
-// tokens, each keeping its own online-softmax state (m, l, acc[D]) in fp32,
-// and the 64 states are merged with wave shuffles at the end.  Semantics are
+// Here one wave serves one (sequence, query head, piece of the context): lanes
+// stride over the piece's tokens, each keeping its own online-softmax state
+// (m, l, acc[D]) in fp32, and the 64 states are merged with wave shuffles.
+// When there are too few (sequence, head) rows to fill the GPU the context is
+// cut into pieces of `tps` tokens, each piece writes an fp32 partial (acc, m,
+// l) to the workspace, and attn_f32_merge combines them.  Semantics are
 // the same as every other decode entry point: contiguous or paged K/V
 // (block-table indirection, kernels/paged_flash_decode_kernel.py:74-84),
 // fp16/bf16 or int8 K/V with per-token scales folded as qk * s_k and
 // p * s_v (kernels/flash_decode_int8_kernel.py:98,111-112), kv_len shared or
 // per sequence, an empty prefix giving zeros.
+#include <string.h>
+
+#include <algorithm>
+
+#include "attn_f32.hpp"
 #include "decode_launch.hpp"
 
 namespace sia {
@@ -43,22 +51,25 @@ __device__ __forceinline__ void load_row<I8>(const char* p, float* x, int n) {
 }
 
 template <int D, class KV, class QT, class ST>
-__global__ __launch_bounds__(256) void decode_small(const DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_small(const DecodeArgs a, const int nsplit, const int tps,
+                                                   float* const part) {
   static_assert(D == 16 || D == 32, "small head dims only");
   constexpr bool kInt8 = std::is_same<KV, I8>::value;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);   // (b, hq)
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);  // (b, hq, piece), pieces fastest
   const int lane = threadIdx.x & 63;
-  if (row >= a.B * a.Hq) return;                            // whole waves leave together
+  if (item >= a.B * a.Hq * nsplit) return;                 // whole waves leave together
+  const int row = item / nsplit, piece = item - row * nsplit;
   const int b = row / a.Hq, hq = row - b * a.Hq, hkv = hq / a.G;
   float q[D];
   load_row<QT>(a.q + b * a.q_sb + (int64_t)hq * a.q_sh, q, D);
   const int n = seq_tokens(a, b);
+  const int t_lo = piece * tps, t_hi = min(n, t_lo + tps);   // this wave's tokens
   const bool paged = a.bt != nullptr;
   const int page = kTile << a.lg_tiles_per_page;
   float m = -INFINITY, l = 0.f, acc[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) acc[d] = 0.f;
-  for (int t = lane; t < n; t += 64) {
+  for (int t = t_lo + lane; t < t_hi; t += 64) {
     int64_t base = 0;
     int pos = t;
     if (paged) {
@@ -106,25 +117,58 @@ __global__ __launch_bounds__(256) void decode_small(const DecodeArgs a) {
     for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
     if (lane == d) mine = x;
   }
-  if (lane < D) {
-    const float inv = 1.0f / (l == 0.f ? 1.f : l);
-    store_out(QT{}, a.out + b * a.o_sb + (int64_t)hq * a.o_sh + lane * (int)sizeof(uint16_t), mine * inv);
+  if (nsplit == 1) {
+    if (lane < D) {
+      const float inv = 1.0f / (l == 0.f ? 1.f : l);
+      store_out(QT{}, a.out + b * a.o_sb + (int64_t)hq * a.o_sh + lane * (int)sizeof(uint16_t), mine * inv);
+    }
+  } else {
+    // partial (acc[D], M, l) of this piece, relative to its max M (-inf: no key)
+    float* dst = part + (int64_t)item * (D + 4);
+    if (lane < D) dst[lane] = mine;
+    if (lane == D) dst[D] = M;
+    if (lane == D + 1) dst[D + 1] = l;
   }
 }
 
 template <class KV, class QT, class ST>
 int launch_decode_small(DecodeLaunch& L) {
-  const int rows = L.a.B * L.a.Hq;
-  const dim3 grid((unsigned)((rows + 3) / 4));
+  const int64_t rows = (int64_t)L.a.B * L.a.Hq;
+  // Pieces per row: enough waves for two per SIMD when the rows alone are
+  // fewer, pieces of at least 256 tokens (4 per lane), and partials that fit
+  // the caller's workspace (the lengths stay on the device: the cut is made
+  // from the cache capacity, so one captured graph serves every length).
+  const int64_t cap = L.a.cap_tokens > 0 ? L.a.cap_tokens : 1;
+  const int cus = device_info().cus > 0 ? device_info().cus : 256;
+  int64_t nsplit = (8LL * cus + rows - 1) / rows;
+  nsplit = std::min<int64_t>(nsplit, (cap + 255) / 256);
+  const int64_t room = (int64_t)(L.ws_bytes / f32_partial_bytes(rows, 1, L.D));
+  nsplit = std::max<int64_t>(1, std::min<int64_t>(nsplit, room));
+  int64_t tps = (cap + nsplit - 1) / nsplit;
+  tps = (tps + 63) / 64 * 64;
+  nsplit = (cap + tps - 1) / tps;
+  if (rows * nsplit > 0x7fffffff || tps > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "too many decode rows");
+  const int64_t waves = rows * nsplit;
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  float* part = (float*)L.ws;
   if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
-  if (L.D == 16) hipLaunchKernelGGL((decode_small<16, KV, QT, ST>), grid, dim3(256), 0, L.stream, L.a);
-  else hipLaunchKernelGGL((decode_small<32, KV, QT, ST>), grid, dim3(256), 0, L.stream, L.a);
+  if (L.D == 16)
+    hipLaunchKernelGGL((decode_small<16, KV, QT, ST>), grid, dim3(256), 0, L.stream, L.a, (int)nsplit, (int)tps, part);
+  else
+    hipLaunchKernelGGL((decode_small<32, KV, QT, ST>), grid, dim3(256), 0, L.stream, L.a, (int)nsplit, (int)tps, part);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "small decode launch: %s", hipGetErrorString(e));
   if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
-  return SIA_OK;
+  if (nsplit == 1) return SIA_OK;
+  F32Args m;
+  memset(&m, 0, sizeof(m));
+  m.B = L.a.B; m.Hq = L.a.Hq; m.Tq = 1;
+  m.nsplit = (int)nsplit;
+  m.part = part;
+  m.out = L.a.out; m.o_sb = L.a.o_sb; m.o_sh = L.a.o_sh; m.o_sm = 0;
+  return launch_attn_merge(m, L.D, L.q_dtype, L.stream);
 }
 
 #define SIA_SMALL(KV, QT, ST) template int launch_decode_small<KV, QT, ST>(DecodeLaunch&);

@@ -180,7 +180,7 @@ def test_paged_small(gpu_pkg, kv, page):
 @pytest.mark.parametrize("kv", ["fp16", "int8"])
 @pytest.mark.parametrize("D", [16, 32])
 def test_paged_small_head_dims(gpu_pkg, kv, D):
-    """head_dim 16 / 32 (wave-per-row kernel): paged, ragged lengths incl. an empty sequence."""
+    """head_dim 16 / 32 (vector path): paged, ragged lengths incl. an empty sequence."""
     announce(f"paged {kv} D={D}")
     q_dtype = torch.float16 if kv == "fp16" else torch.bfloat16
     case = _syn().paged_case([500, 0, 16, 129], Hq=8, Hkv=2, D=D, page=16, seed=21, device=DEV, kv=kv,
@@ -189,6 +189,20 @@ def test_paged_small_head_dims(gpu_pkg, kv, D):
     torch.cuda.synchronize()
     assert_close(out, oracle_paged(case), 2e-3, f"paged {kv} D={D}")
     assert torch.all(out[1] == 0)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "int8"])
+@pytest.mark.parametrize("D", [16, 32])
+def test_small_head_dims_long_context(gpu_pkg, kv, D):
+    """head_dim 16 / 32 at small batch and long context: the vector path splits the
+    context over many work-groups and merges the pieces (one row of a long sequence
+    must not be left to a single wave)."""
+    announce(f"small head dim long context {kv} D={D}")
+    case = _syn().paged_case([9000, 1234], Hq=8, Hkv=2, D=D, page=16, seed=23, device=DEV, kv=kv,
+                             q_dtype=torch.bfloat16)
+    out = run_paged(gpu_pkg, case)
+    torch.cuda.synchronize()
+    assert_close(out, oracle_paged(case), 2e-3, f"long context {kv} D={D}")
 
 
 @pytest.mark.parametrize("ratio", [1.0, 100.0, 1000.0])
