@@ -566,9 +566,11 @@ def main(argv=None):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int8",
-        "dtype_detail": "int8 K/V (QK on int8 MFMA, exact int32 dots), bf16 q/out, f16 PV MFMA, fp32 softmax/accumulate",
-        "data": "synthetic (seeded N(0,1) K/V quantised per token per head; random page permutation)",
+        "dtype": "int8" if case.is_int8 else "fp16",
+        "dtype_detail": ("int8 K/V (QK on int8 MFMA, exact int32 dots), bf16 q/out, f16 PV MFMA, fp32 softmax/accumulate"
+                         if case.is_int8 else "fp16 q/K/V/out, f16 MFMA, fp32 softmax/accumulate"),
+        "data": ("synthetic (seeded N(0,1) K/V quantised per token per head; random page permutation)" if case.is_int8
+                 else "synthetic (seeded N(0,1) q/K/V; random page permutation)"),
         "config": {
             "workload": {"cfg2": "config 2: paged fp16 decode B16 ctx U[256,4096]",
                          "cfg3": "config 3: paged INT8-KV GQA decode B64 ctx 8192",
@@ -618,7 +620,7 @@ def main(argv=None):
         case = None
 
     if not args.no_cpu_baseline:
-        if case is None:
+        if case is None or not case.is_int8:   # the CPU baseline is the headline (config 3) path
             case = syn.cfg3(dev)
         print("[bench] timing the CPU baseline sample", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(case, args.cpu_seconds)

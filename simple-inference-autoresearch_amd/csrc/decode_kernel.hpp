@@ -79,6 +79,10 @@ struct DecodeArgs {
 
 // --------------------------------------------------------------------- plan
 
+// Batches up to this size keep their per-sequence token counts in LDS after
+// the plan (4 bytes each), so a segment's length needs no second global read.
+constexpr int kLensInLds = 4096;
+
 __device__ __forceinline__ int seq_tiles(const DecodeArgs& a, int b) {
   int n = a.kv_len[a.kv_per_seq ? b : 0];
   n = n < 0 ? 0 : (n > a.cap_tokens ? a.cap_tokens : n);
@@ -178,7 +182,12 @@ __device__ int plan_work(const DecodeArgs& a, int* pre, int* red, int tok0) {
     __syncthreads();
     return a.B * per;
   }
-  for (int b = threadIdx.x; b < a.B; b += T) pre[b] = seq_tiles(a, b);
+  int* lens = pre + a.B + 1;                 // token counts, kept for the segments (small batches)
+  for (int b = threadIdx.x; b < a.B; b += T) {
+    const int n = seq_tokens(a, b);
+    pre[b] = (n + kTile - 1) / kTile;
+    if (a.B <= kLensInLds) lens[b] = n;
+  }
   __syncthreads();
   block_scan<NW>(a, 1, pre, red, a.UB);
   return pre[a.B];
@@ -604,7 +613,7 @@ void decode_main(const DecodeArgs a) {
   constexpr int E = D / 16;
   constexpr int KSTEPS = D / 32;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  // LDS: [acc: NW*G16*D f32][m: NW*G16][l: NW*G16][red: 2*NW+2 ints][pre: B+1 ints]
+  // LDS: [acc: NW*G16*D f32][m: NW*G16][l: NW*G16][red: 2*NW+2 ints][pre: B+1 ints][lens: B ints, B <= kLensInLds]
   float* l_acc = (float*)smem;
   float* l_m = l_acc + NW * a.G16 * D;
   float* l_l = l_m + NW * a.G16;
@@ -658,8 +667,9 @@ void decode_main(const DecodeArgs a) {
     int blo = 0, bhi = a.B;
     while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= x) blo = mid; else bhi = mid; }
     const int b = uniform(blo);
-    // (a batch-wide length was read once already; per-sequence ones are read here)
-    const int ntok = a.kv_per_seq ? uniform(seq_tokens(a, b)) : tok0;
+    // (a batch-wide length was read once already; per-sequence ones were kept
+    // in LDS by the plan for batches up to kLensInLds, else are read again)
+    const int ntok = a.kv_per_seq ? uniform(a.B <= kLensInLds ? pre[a.B + 1 + b] : seq_tokens(a, b)) : tok0;
     const int ntile = (ntok + kTile - 1) / kTile;
     const int rem = uniform(x - pre[b]);
     const int ublk = rem / ntile;

@@ -31,7 +31,7 @@ struct DecodeLaunch {
 
 inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
   return (size_t)NW * G16 * D * 4 + (size_t)2 * NW * G16 * 4 + (size_t)(2 * NW + 2) * 4 +
-         (size_t)(B + 1) * 4;
+         (size_t)(B + 1) * 4 + (B <= kLensInLds ? (size_t)B * 4 : 0);
 }
 
 template <int D, class KV, class QT, class ST>
