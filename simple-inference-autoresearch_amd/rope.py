@@ -45,21 +45,6 @@ def _check_cos_sin(cos: torch.Tensor, sin: torch.Tensor, head_dim: int) -> int:
     return cos.stride(0)
 
 
-def _row_stride(x: torch.Tensor, T: int, head_dim: int):
-    """Stride between the flattened ``B*T`` rows of ``x``, or None when rows are not uniformly spaced.
-
-    A size-1 dim's stride is never used (torch calls such views contiguous
-    whatever that stride is).
-    """
-    if x.stride(-1) != 1 or (x.shape[2] > 1 and x.stride(2) != head_dim):
-        return None
-    if T == 1:
-        return x.stride(0)
-    if x.shape[0] == 1 or x.stride(0) == T * x.stride(1):
-        return x.stride(1)
-    return None
-
-
 def rope_triton(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                 interleaved: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """Rotate ``q (B, T, Hq, D)`` and ``k (B, T, Hkv, D)`` by the ``cos``/``sin`` tables.
@@ -69,22 +54,17 @@ def rope_triton(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.
     (Llama/NeoX), ``True`` pairs ``(2i, 2i+1)`` (GPT-J).  Returns contiguous
     ``(q_rot, k_rot)`` with the inputs' shapes and dtypes.
     """
-    head_dim = q.shape[-1]
-    _check_cos_sin(cos, sin, head_dim)
     B, T, n_heads_q, head_dim = q.shape
+    _check_cos_sin(cos, sin, head_dim)
     if head_dim % 2:
         raise AssertionError("head_dim must be even for RoPE")
-    if not (k.shape[0] == B and k.shape[1] == T and k.shape[3] == head_dim):
-        raise AssertionError(f"k {tuple(k.shape)} does not match q {tuple(q.shape)} in B, T or head_dim")
-    if sin.shape[0] != cos.shape[0]:
-        raise AssertionError("cos and sin must have the same number of rows")
-    ops = _lib.gpu_ops()
-    if _row_stride(q, T, head_dim) is None:
-        q = q.contiguous()
-    if _row_stride(k, T, head_dim) is None:
-        k = k.contiguous()
-    # outputs are allocated contiguous in C++ (the inputs' shapes and dtypes)
-    return ops.rope_qk(q, k, cos, sin, bool(interleaved))
+    ks = k.shape
+    if ks[0] != B or ks[1] != T or ks[3] != head_dim:
+        raise AssertionError(f"k {tuple(ks)} does not match q {tuple(q.shape)} in B, T or head_dim")
+    # views whose B*T rows are not one stride apart (head_dim unit-stride,
+    # heads head_dim apart, stride(0) == T*stride(1) unless T == 1 or B == 1)
+    # are copied by the extension op, which also allocates the outputs
+    return _lib.gpu_ops().rope_qk(q, k, cos, sin, bool(interleaved))
 
 
 def apply_rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):

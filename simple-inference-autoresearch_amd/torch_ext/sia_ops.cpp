@@ -257,10 +257,22 @@ OptT rope_kv_write(const OptT& q, const Tensor& k, const OptT& v, const Tensor& 
   return qo;
 }
 
-std::tuple<Tensor, Tensor> rope_qk(const Tensor& q, const Tensor& k, const Tensor& cos, const Tensor& sin,
+// A (B, T, H, D) view whose B*T rows sit one stride apart (head_dim
+// unit-stride, heads D apart), as sia_rope_qk reads it; other views are
+// copied first (kernels/rope_kernel.py:216-235 does the same).
+bool rows_flattenable(const Tensor& x) {
+  if (x.dim() != 4) return true;   // the C ABI reports the shape error
+  const int64_t T = x.size(1), H = x.size(2), D = x.size(3);
+  if (x.stride(3) != 1 || (H > 1 && x.stride(2) != D)) return false;
+  return T == 1 || x.size(0) == 1 || x.stride(0) == T * x.stride(1);
+}
+
+std::tuple<Tensor, Tensor> rope_qk(const Tensor& q_in, const Tensor& k_in, const Tensor& cos, const Tensor& sin,
                                    bool interleaved) {
-  const at::Device dev = gpu_of(q, "q");
+  const at::Device dev = gpu_of(q_in, "q");
   const c10::DeviceGuard guard(dev);
+  const Tensor q = rows_flattenable(q_in) ? q_in : q_in.contiguous();
+  const Tensor k = rows_flattenable(k_in) ? k_in : k_in.contiguous();
   const sia_tensor dq = desc(q, dev, "q"), dk = desc(k, dev, "k"), dc = desc(cos, dev, "cos"),
                    dsn = desc(sin, dev, "sin");
   Tensor qo = at::empty(q.sizes(), q.options());
