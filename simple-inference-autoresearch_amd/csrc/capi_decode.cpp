@@ -242,7 +242,9 @@ int dispatch_f32(const DecodeLaunch& D, const Geometry& g, int kv_dtype, const s
   a.ncol = g.G;
   a.nchunk = (g.G + kF32Cols - 1) / kF32Cols;
   a.qk_scale = d.qk_scale;
-  // split: enough items for four per CU, pieces of >= 256 keys, within the workspace
+  // split: enough items for four per CU, pieces of >= 128 keys (two steps of a
+  // work-group: shorter pieces measured slower, longer ones leave small calls
+  // to a few work-groups), within the workspace
   const int64_t rows = (int64_t)g.B * g.Hq;
   const int64_t base = (int64_t)g.B * g.Hkv * a.nchunk;
   const int64_t cap = a.cap > 0 ? a.cap : 1;
@@ -253,7 +255,7 @@ int dispatch_f32(const DecodeLaunch& D, const Geometry& g, int kv_dtype, const s
     const int cus = device_info().cus > 0 ? device_info().cus : 256;
     int64_t want = (4LL * cus + base - 1) / base;
     want = want < 1 ? 1 : want;
-    const int64_t most = (cap + 255) / 256;
+    const int64_t most = (cap + 127) / 128;
     if (want > most) want = most;
     tps = (cap + want - 1) / want;
   }
