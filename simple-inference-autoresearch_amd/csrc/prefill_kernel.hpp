@@ -453,12 +453,13 @@ void prefill_fwd(const PrefillArgs a) {
   // buffer range: the hardware drops every out-of-range read (no memory
   // traffic) and what it fills is never read, so every wave issues the same
   // instruction count per group and the waits below are constants.
-  auto issue_k = [&](int blk, char* LK) {
+  // (one transfer instruction each: the ring refills are spread over the
+  // MFMA stream, see `qk`)
+  auto issue_k1 = [&](int blk, char* LK, int i) {
     const bool live = blk < nblk;
     const int key0 = live ? blk * kPfBN : 0;
     const int rows = live ? min(kPfBN, a.Tk - key0) : 0;
-#pragma unroll
-    for (int i = 0; i < NK; ++i) {
+    {
       const int c = wave * NK + i;
       const bool real = c < C::kdma;
       const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
@@ -471,10 +472,9 @@ void prefill_fwd(const PrefillArgs a) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, dst, 16, voff, 0, 0, 0);
     }
   };
-  auto issue_v = [&](int blk, char* LV) {
+  auto issue_v1 = [&](int blk, char* LV, int i) {
     const bool live = blk < nblk;
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
+    {
       const int c = wave * NV + i;
       const bool real = c < C::vdma;
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -485,6 +485,19 @@ void prefill_fwd(const PrefillArgs a) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, dst, 16, voff, soff, 0, 0);
     }
   };
+  auto issue_k = [&](int blk, char* LK) {
+#pragma unroll
+    for (int i = 0; i < NK; ++i) issue_k1(blk, LK, i);
+  };
+  auto issue_v = [&](int blk, char* LV) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) issue_v1(blk, LV, i);
+  };
+  // A work step's ring refill: NP single transfers (K pieces, then V
+  // pieces), issued from inside its QK product so that the memory pipeline
+  // takes them while the MFMAs run (issued back to back after the barrier,
+  // the eight waves' transfers queue up and stall every wave's issue)
+  constexpr int NP = NK + NV;
 
   f32x16 o[ET];
 #pragma unroll
@@ -493,7 +506,9 @@ void prefill_fwd(const PrefillArgs a) {
 
   // S^T = K Q^T for the 64 keys of one K stage: two 32-key tiles (raw scores;
   // the scale is folded into the exponent, c > 0 keeps the max)
-  auto qk = [&](const char* K, f32x16& s0, f32x16& s1) {
+  // (piece(p) issues transfer p of the step's ring refill; transfer p goes
+  // after k-step p KST / NP)
+  auto qk = [&](const char* K, f32x16& s0, f32x16& s1, auto piece) {
     s0 = f32x16{};
     s1 = f32x16{};
 #pragma unroll
@@ -502,8 +517,12 @@ void prefill_fwd(const PrefillArgs a) {
       const u32x4 a1 = *(const u32x4*)(K + k_rd[j] + 32 * RB);
       s0 = mfma32x32x16(T{}, a0, qop[j], s0);
       s1 = mfma32x32x16(T{}, a1, qop[j], s1);
+#pragma unroll
+      for (int p = 0; p < NP; ++p)
+        if ((p * KST) / NP == j) piece(p);
     }
   };
+  auto no_piece = [](int) {};
   // keys past this lane's last visible key -> -inf (diagonal / ragged blocks)
   auto mask = [&](f32x16& s0, f32x16& s1, int key0) {
 #pragma unroll
@@ -581,15 +600,20 @@ void prefill_fwd(const PrefillArgs a) {
   // The work of one key block j (sa = raw scores of block j in, sb = scores
   // of block j + 1 out): the MFMAs of S_{j+1} run under the softmax of
   // block j, then the PV MFMAs of block j.
-  auto work = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1, float& rmax) {
+  auto work = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1, float& rmax,
+                  auto piece) {
     constexpr int P = decltype(parity)::value;           // j % S, known at compile time
-    if (j < wblk) {
+    if (j >= wblk) {
+      // (a wave past its last block still moves its share of the ring)
+#pragma unroll
+      for (int p = 0; p < NP; ++p) piece(p);
+    } else {
       raise_max(rmax);
       // S_{j+1} is computed even on the wave's last block (its stage then
       // holds another block or stale keys and the scores are discarded):
       // one code path keeps the accumulators in place across iterations
       u32x4 pop[4];
-      qk(kstage(PfParity<P + 1>{}), sb0, sb1);
+      qk(kstage(PfParity<P + 1>{}), sb0, sb1, piece);
       numer(sa0, sa1, pop);
       pv(vstage(PfParity<P>{}), pop);
       // the next block's row max (unmasked; redone below on masked blocks)
@@ -601,6 +625,11 @@ void prefill_fwd(const PrefillArgs a) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one S MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // next operand read
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // softmax VALU
+        if (i % 2 == 1) {
+#pragma unroll
+          for (int p = 0; p < NP; ++p)                        // the ring transfers after this k-step
+            if ((p * KST) / NP == i / 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4 * ET; ++i) {
@@ -619,7 +648,7 @@ void prefill_fwd(const PrefillArgs a) {
   float rmax = -INFINITY;
   auto first_scores = [&]() {
     if (wblk > 0) {
-      qk(lk0, s0, s1);
+      qk(lk0, s0, s1, no_piece);
       if (wfull == 0) mask(s0, s1, 0);
       rmax = rowmax(s0, s1);
     }
@@ -628,19 +657,31 @@ void prefill_fwd(const PrefillArgs a) {
   if constexpr (S == 4) {
     // Four-stage ring, one barrier per two key blocks.  Block j needs K_{j+1}
     // (scores of the next block) and V_j.  The barrier before blocks j, j+1
-    // (j even) retires blocks j-2, j-1, then refills the stages they read
-    // with K_{j+3}, K_{j+4}, V_{j+2}, V_{j+3}: two blocks of lead, waited
-    // for (vmcnt(0)) at the next barrier.
+    // (j even) retires blocks j-2, j-1; the stages they read are refilled
+    // with K_{j+3}, K_{j+4}, V_{j+2}, V_{j+3} from inside the two blocks'
+    // QK products: two blocks of lead, waited for (vmcnt(0)) at the next
+    // barrier.
     auto super = [&](auto parity, int j, bool second) {
       constexpr int P = decltype(parity)::value;          // 0 or 2
       wait_vmcnt(0);                                      // this wave's DMA of blocks j, j+1 landed
       ring_barrier();                                     // everyone's landed; blocks j-2, j-1 retired
-      issue_k(j + 3, kstage(PfParity<P + 3>{}));
-      issue_v(j + 2, vstage(PfParity<P + 2>{}));
-      issue_k(j + 4, kstage(PfParity<P>{}));
-      issue_v(j + 3, vstage(PfParity<P + 3>{}));
-      work(PfParity<P>{}, j, s0, s1, n0, n1, rmax);
-      if (second) work(PfParity<P + 1>{}, j + 1, n0, n1, s0, s1, rmax);
+      // refills: K_{j+3}, V_{j+2} from block j's QK, K_{j+4}, V_{j+3} from
+      // block j+1's (all into stages retired at this barrier)
+      auto piece0 = [&](int p) {
+        if (p < NK) issue_k1(j + 3, kstage(PfParity<P + 3>{}), p);
+        else issue_v1(j + 2, vstage(PfParity<P + 2>{}), p - NK);
+      };
+      auto piece1 = [&](int p) {
+        if (p < NK) issue_k1(j + 4, kstage(PfParity<P>{}), p);
+        else issue_v1(j + 3, vstage(PfParity<P + 3>{}), p - NK);
+      };
+      work(PfParity<P>{}, j, s0, s1, n0, n1, rmax, piece0);
+      if (second) {
+        work(PfParity<P + 1>{}, j + 1, n0, n1, s0, s1, rmax, piece1);
+      } else {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) piece1(p);
+      }
     };
     if (nblk > 0) {
       issue_k(0, lk0);
@@ -667,14 +708,17 @@ void prefill_fwd(const PrefillArgs a) {
     if (j + 2 < nblk) super(PfParity<2>{}, j + 2, false);
   } else {
     // Two-stage ring, one barrier per block: the barrier before block j
-    // retires block j - 1 and refills its stages with K_{j+2} and V_{j+1}.
+    // retires block j - 1, whose stages block j's QK product refills with
+    // K_{j+2} and V_{j+1}.
     auto step = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1) {
       constexpr int P = decltype(parity)::value;
       wait_vmcnt(0);                                      // this wave's part of K_{j+1}, V_j landed
       ring_barrier();
-      issue_k(j + 2, kstage(PfParity<P>{}));
-      issue_v(j + 1, vstage(PfParity<P + 1>{}));
-      work(parity, j, sa0, sa1, sb0, sb1, rmax);
+      auto piece = [&](int p) {                          // K_{j+2}, V_{j+1} into the stages retired here
+        if (p < NK) issue_k1(j + 2, kstage(PfParity<P>{}), p);
+        else issue_v1(j + 1, vstage(PfParity<P + 1>{}), p - NK);
+      };
+      work(parity, j, sa0, sa1, sb0, sb1, rmax, piece);
     };
     if (nblk > 0) {
       issue_k(0, lk0);
