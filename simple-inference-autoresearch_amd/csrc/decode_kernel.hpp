@@ -884,32 +884,40 @@ void decode_main(const DecodeArgs a) {
 
 // Merge split-K partials: each (sequence, query head) row is handled by D/4
 // lanes holding 4 outputs each (16-byte partial loads), so a wave merges
-// 64/(D/4) rows.  Pass 1 takes the max m over the splits (one split per
-// lane of the row's group, repeated per D/4 splits); pass 2 forms the split
-// weights 2^(m_s - M) a group at a time, broadcasts each within the group and
-// accumulates the weighted partials.  Loop bounds are uniform over the wave
-// (the largest split count of its rows), so every shuffle sees all lanes.
-// Rows of sequences the main kernel wrote directly are skipped; empty
-// sequences are written as zeros.
+// 64/(D/4) rows.  A row's pieces are merged online, up to kRedBatch at a
+// time (the batch is sized to the wave's remaining piece count): every lane
+// loads the batch's (m, l) pairs and its slices of their partials together
+// (one memory round trip per batch; the merge is latency-bound, a few MB
+// spread over few rows), rescales its running (M, L, acc) to the batch's max
+// and adds the pieces with weights 2^(m_s - M).  Loop bounds
+// are uniform over the wave (the largest piece count of its rows).  Rows of
+// sequences the main kernel wrote directly are skipped; empty sequences are
+// written as zeros.
+constexpr int kRedBatch = 16;
+// Waves per work-group of decode_reduce: one, so that the few hundred rows
+// of a small batch spread over every CU instead of a quarter of them.
+constexpr int kRedWaves = 1;
+
 template <int D, class OT, int NW>
-__global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
+__global__ __launch_bounds__(kRedWaves * 64) void decode_reduce(const DecodeArgs a) {
   constexpr int LPR = D / 4;          // lanes per row
   constexpr int RPW = 64 / LPR;       // rows per wave
   const int lane = threadIdx.x & 63;
   const int li = lane % LPR;
-  const int gbase = lane - li;        // first lane of this row's group
-  const int row = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int row = (blockIdx.x * kRedWaves + (threadIdx.x >> 6)) * RPW + lane / LPR;
   const bool inr = row < a.B * a.Hq;
+  // the plan's header and this row's prefix entries in one round trip
+  // (loaded before any test of them, for rows past the end as well)
+  const int b = (inr ? row : 0) / a.Hq;
+  const int hq = (inr ? row : 0) - b * a.Hq;
+  const int pb = a.ws_plan[kPlanHeader + b], pe = a.ws_plan[kPlanHeader + b + 1];
   const int W = a.ws_plan[kPlanW], G = a.ws_plan[kPlanG];
   // pieces of this row's (sequence, unit block): one per work-group in
   // [gf, gf + nsplit); the first group's piece is its first segment (slot
   // 2g) only if the range starts exactly at the group's start
-  int nsplit = 1, gf = 0, s_first = 0, b = 0, hq = 0, uin = 0, cc = 0;
+  int nsplit = 1, gf = 0, s_first = 0, uin = 0, cc = 0;
   if (inr) {
-    b = row / a.Hq;
-    hq = row - b * a.Hq;
-    const int pb = a.ws_plan[kPlanHeader + b];
-    const int ntile = (a.ws_plan[kPlanHeader + b + 1] - pb) / a.UB;
+    const int ntile = (pe - pb) / a.UB;
     const int hkv = hq / a.G, gi = hq - hkv * a.G;
     cc = gi & 15;
     const int unit = hkv * a.HG + (gi >> 4);
@@ -934,49 +942,51 @@ __global__ __launch_bounds__(256) void decode_reduce(const DecodeArgs a) {
     const int id = 2 * (gf + s) + (s == 0 ? s_first : 0);
     return ((int64_t)id * NW + uin) * a.G16 + cc;
   };
-  auto group_max = [&](float x) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-    return x;
-  };
-  auto group_sum = [&](float x) {
-#pragma unroll
-    for (int o = LPR / 2; o > 0; o >>= 1) x += __shfl_xor(x, o);
-    return x;
-  };
-  float M = -INFINITY;
-  for (int s0 = 0; s0 < nmax; s0 += LPR) {
-    const int s = s0 + li;
-    M = fmaxf(M, (work && s < nsplit) ? a.ws_ml[slot(s) * 2] : -INFINITY);
-  }
-  M = group_max(M);
+  float M = -INFINITY, L = 0.f;
   f32x4 A = {0.f, 0.f, 0.f, 0.f};
-  float L = 0.f;
-  for (int s0 = 0; s0 < nmax; s0 += LPR) {
-    const int s = s0 + li;
-    float w = 0.f;
-    if (work && s < nsplit && M != -INFINITY) {
-      const float m = a.ws_ml[slot(s) * 2];
-      w = m == -INFINITY ? 0.f : fast_exp2(m - M);
-      L += w * a.ws_ml[slot(s) * 2 + 1];
-    }
-    // eight partial loads in flight at a time (a row can have tens of splits)
-    const int n = min(LPR, nmax - s0);
-    for (int j0 = 0; j0 < n; j0 += 8) {
-      f32x4 x[8];
-      float wj[8];
+  // Merge pieces [s0, s0 + K).  Every load is issued: a piece past the row's
+  // count reads the row's first piece and a lane with no merge to do reads
+  // slot 0 (one address per instruction), and both are masked once loaded.
+  auto batch = [&](int s0, auto kk) {
+    constexpr int K = decltype(kk)::value;
+    float m[K], l[K];
+    f32x4 x[K];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        const int j = j0 + t;
-        const bool ok = work && j < n && s0 + j < nsplit;
-        x[t] = ok ? *(const f32x4*)(a.ws_acc + slot(s0 + j) * D + 4 * li) : f32x4{0.f, 0.f, 0.f, 0.f};
-        wj[t] = __shfl(w, gbase + (j & (LPR - 1)));
-      }
-#pragma unroll
-      for (int t = 0; t < 8; ++t) A += wj[t] * x[t];
+    for (int k = 0; k < K; ++k) {
+      const int64_t sl = work ? slot(s0 + k < nsplit ? s0 + k : 0) : 0;
+      const float2 ml = *(const float2*)(a.ws_ml + sl * 2);
+      m[k] = ml.x;
+      l[k] = ml.y;
+      x[k] = *(const f32x4*)(a.ws_acc + sl * D + 4 * li);
     }
+    __builtin_amdgcn_sched_barrier(0);   // all of the batch's loads before the first use
+    float mb = M;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (!(work && s0 + k < nsplit)) m[k] = -INFINITY;
+      mb = fmaxf(mb, m[k]);
+    }
+    // branch-free, so that no load is moved behind a test of the maxima:
+    // 2^-inf = 0 weighs out masked pieces and the empty state (M = -inf)
+    const float mref = mb == -INFINITY ? 0.f : mb;
+    const float r = fast_exp2(M - mref);
+    L *= r;
+    A *= r;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const float w = fast_exp2(m[k] - mref);
+      L += w * l[k];
+      A += w * x[k];
+    }
+    M = mb;
+  };
+  for (int s0 = 0; s0 < nmax; s0 += kRedBatch) {
+    const int rem = nmax - s0;   // wave-uniform
+    if (rem <= 2) batch(s0, std::integral_constant<int, 2>{});
+    else if (rem <= 4) batch(s0, std::integral_constant<int, 4>{});
+    else if (rem <= 8) batch(s0, std::integral_constant<int, 8>{});
+    else batch(s0, std::integral_constant<int, kRedBatch>{});
   }
-  L = group_sum(L);
   if (!work) return;
   const float inv = 1.0f / (L == 0.f ? 1.f : L);
   char* op = a.out + b * a.o_sb + (int64_t)hq * a.o_sh + 4 * li * (int)sizeof(uint16_t);

@@ -55,9 +55,9 @@ int launch_decode_typed(DecodeLaunch& L) {
   if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
   const int rows = L.a.B * L.a.Hq;
-  constexpr int kRowsPerGroup = 4 * (64 / (D / 4));   // 4 waves, 64 / (D/4) rows each
-  hipLaunchKernelGGL((decode_reduce<D, QT, NW>), dim3((rows + kRowsPerGroup - 1) / kRowsPerGroup), dim3(256), 0,
-                     L.stream, L.a);
+  constexpr int kRowsPerGroup = kRedWaves * (64 / (D / 4));   // 64 / (D/4) rows per wave
+  hipLaunchKernelGGL((decode_reduce<D, QT, NW>), dim3((rows + kRowsPerGroup - 1) / kRowsPerGroup),
+                     dim3(kRedWaves * 64), 0, L.stream, L.a);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode reduce launch: %s", hipGetErrorString(e));
   return SIA_OK;
