@@ -175,6 +175,9 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   const int64_t groups = (int64_t)a.nqblk * B * Hkv;   // work-groups come in runs of G sharing a KV head
   if (groups * a.G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "grid too large");
   a.remap = groups % 8 == 0;
+  a.dG = make_fastdiv((uint32_t)a.G);
+  a.dHkv = make_fastdiv((uint32_t)Hkv);
+  a.dB = make_fastdiv((uint32_t)B);
   if (rope != nullptr && (rc = setup_rope(*rope, B, Tq, D, q->dtype, a))) return rc;
 
   PackArgs& p = L.pack;

@@ -63,6 +63,7 @@ struct PrefillArgs {
   int32_t nqblk;                                // ceil(Tq / 128)
   int32_t nkb;                                  // ceil(Tk / 64)
   int32_t remap;                                // XCD-aware block order
+  FastDiv dG, dHkv, dB;                         // divisions by G, Hkv, B for the block mapping
   // rotary embedding of q at load (prefill_fwd<D, T, true> only): query row
   // i of sequence b sits at position start_host + start_pos[b or 0] + i
   // (start_pos NULL: 0) and is rotated by row pos of the cos/sin tables
@@ -338,19 +339,13 @@ __device__ __forceinline__ float half_swap_sum(float x) {
 // before another wave may refill it.
 __device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// vmcnt(n) for a wave-uniform n in [0, 8] (the immediate must be a constant)
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0f70); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0f71); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0f72); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0f73); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0f74); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0f75); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0f76); break;
-    case 7: __builtin_amdgcn_s_waitcnt(0x0f77); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0f78); break;
-  }
+// vmcnt(N): at most N vector memory instructions of this wave still
+// outstanding (gfx9 s_waitcnt: vmcnt bits 3:0 and 15:14, expcnt and lgkmcnt
+// left at their no-wait maxima)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 
 template <int D, class T, int ROPE>
@@ -384,14 +379,16 @@ void prefill_fwd(const PrefillArgs a) {
   int lin = blockIdx.x;
   if (a.remap) {
     const int xcd = lin & 7, slot = lin >> 3;
-    lin = ((slot / a.G) * 8 + xcd) * a.G + slot % a.G;
+    const int sg = fdiv(slot, a.dG);
+    lin = (sg * 8 + xcd) * a.G + (slot - sg * a.G);
   }
-  const int g = lin % a.G;
-  int rest = lin / a.G;
-  const int hkv = rest % a.Hkv;
-  rest /= a.Hkv;
-  const int b = rest % a.B;
-  const int qblk = a.nqblk - 1 - rest / a.B;
+  int rest = fdiv(lin, a.dG);
+  const int g = lin - rest * a.G;
+  const int r2 = fdiv(rest, a.dHkv);
+  const int hkv = rest - r2 * a.Hkv;
+  const int r3 = fdiv(r2, a.dB);
+  const int b = r2 - r3 * a.B;
+  const int qblk = a.nqblk - 1 - r3;
   const int hq = hkv * a.G + g;
 
   const int lane = threadIdx.x & 63;
@@ -399,24 +396,30 @@ void prefill_fwd(const PrefillArgs a) {
   const int l32 = lane & 31, h = lane >> 5;
   const int off = a.Tk - a.Tq;                           // bottom-right causal offset
   const int q0 = qblk * BM;
-  const int qi = q0 + wave * 32 + l32;                   // this lane's query row
+  // The 32-row group of the work-group's rows this wave owns.  Waves w and
+  // w + 4 share a SIMD; under a causal mask later row groups see more key
+  // blocks, so the second wave of each SIMD takes the groups in reverse
+  // (7, 6, 5, 4) and every SIMD carries the same number of key blocks.
+  const int rg = PfCfg<D>::wpe == 2 && wave >= NW / 2 ? 3 * NW / 2 - 1 - wave : wave;
+  const int qi = q0 + rg * 32 + l32;                     // this lane's query row
 
   // ---- Q^T operand (B of S^T = K Q^T): query qi, d = 16 j + 8 h + [0, 8)
+  // (loaded by load_q below, after the first K block's transfers are issued)
   u32x4 qop[KST];
   RopeQ<D, ROPE> rq;   // rotation inputs (applied once the first K/V transfers are issued)
-  {
+  auto load_q = [&]() {
     const char* qp = a.q + b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)min(qi, a.Tq - 1) * a.q_sm + 16 * h;
 #pragma unroll
-    for (int j = 0; j < KST; ++j) qop[j] = qi < a.Tq ? *(const u32x4*)(qp + 32 * j) : u32x4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < KST; ++j) qop[j] = *(const u32x4*)(qp + 32 * j);   // (rows past Tq read row Tq - 1; never stored)
     if constexpr (ROPE != kRopeNone) {
       const int64_t base = (int64_t)a.start_host + (a.start_pos != nullptr ? a.start_pos[a.pos_per_seq ? b : 0] : 0);
       rope_q_fetch<D, ROPE>(a, rq, base + qi, h);
     }
-  }
+  };
 
   const int kend = a.causal ? min(a.Tk, off + q0 + BM) : a.Tk;
   const int nblk = kend > 0 ? (kend + kPfBN - 1) / kPfBN : 0;   // key blocks of the work-group
-  const int wrow0 = q0 + wave * 32;                      // this wave's first row
+  const int wrow0 = q0 + rg * 32;                        // this wave's first row
   const int wend = a.causal ? min(a.Tk, off + wrow0 + 32) : a.Tk;   // keys this wave can see
   const int wblk = wend > 0 ? min(nblk, (wend + kPfBN - 1) / kPfBN) : 0;   // blocks this wave computes
   // blocks [0, wfull) are visible to every row of the wave: no mask
@@ -530,6 +533,8 @@ void prefill_fwd(const PrefillArgs a) {
   };
   auto no_piece = [](int) {};
   // keys past this lane's last visible key -> -inf (diagonal / ragged blocks)
+  // (each compare feeds its select at once: compares hoisted ahead of the
+  // selects would hold 32 lane masks in scalar registers)
   auto mask = [&](f32x16& s0, f32x16& s1, int key0) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -568,44 +573,17 @@ void prefill_fwd(const PrefillArgs a) {
       for (int e = 0; e < ET; ++e) o[e] *= alpha;
     }
   };
-  // P = 2^(s c - m) rounded to f16, packed as the B operand of the PV product
-  // (k-slot ks holds the keys of S^T output registers 8 (ks % 2) .. + 8 of
-  // tile ks / 2); the row sum is taken over the rounded weights the MFMA
-  // uses, so the output stays an exact convex combination of V rows
-  auto numer = [&](const f32x16& s0, const f32x16& s1, u32x4* pop) {
-    const float mu = m == -INFINITY ? 0.f : m;           // rows with nothing visible yet
-    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int j0 = (ks & 1) * 8 + 2 * i;
-        const float x0 = ks < 2 ? s0[j0] : s1[j0];
-        const float x1 = ks < 2 ? s0[j0 + 1] : s1[j0 + 1];
-        const float p0 = fast_exp2(__builtin_fmaf(x0, a.qk_scale, -mu));
-        const float p1 = fast_exp2(__builtin_fmaf(x1, a.qk_scale, -mu));
-        const uint32_t w = pack2(F16{}, p0, p1);
-        l = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, l, false);
-        pop[ks][i] = w;
-      }
-    }
-  };
-  // O^T += V^T P^T: operand chunk 2 ks + h of dimension 32 e + l32
-  auto pv = [&](const char* V, const u32x4* pop) {
-    const char* vr = V + h * DV * 16 + l32 * 16;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-      for (int e = 0; e < ET; ++e) {
-        const u32x4 va = *(const u32x4*)(vr + ks * 2 * DV * 16 + e * 512);
-        o[e] = mfma32x32x16(F16{}, va, pop[ks], o[e]);
-      }
-    }
-  };
-
   // The work of one key block j (sa = raw scores of block j in, sb = scores
-  // of block j + 1 out): the MFMAs of S_{j+1} run under the softmax of
-  // block j, then the PV MFMAs of block j.
+  // of block j + 1 out): the QK MFMAs of S_{j+1} and the PV MFMAs of block j
+  // form one stream of NS MFMA slots, each reading its A operand from LDS
+  // two slots ahead (an LDS read takes ~64 cycles, one MFMA slot of a wave
+  // ~48 with two waves per SIMD, so a read issued one slot ahead stalls
+  // every MFMA).  The exponentials of block j run under the QK slots
+  // (P_j k-slots 0-2) and the first PV slots (k-slot 3), whose MFMAs need
+  // them in that order; the next block's row max, which needs all of
+  // S_{j+1}, fills the last PV slots.
+  constexpr int NQK = 2 * KST, NPV = 4 * ET, NS = NQK + NPV;
+  constexpr int PD = 2;                                  // LDS operand reads in flight ahead of the MFMA
   auto work = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1, float& rmax,
                   auto piece) {
     constexpr int P = decltype(parity)::value;           // j % S, known at compile time
@@ -618,32 +596,100 @@ void prefill_fwd(const PrefillArgs a) {
       // S_{j+1} is computed even on the wave's last block (its stage then
       // holds another block or stale keys and the scores are discarded):
       // one code path keeps the accumulators in place across iterations
+      const char* K = kstage(PfParity<P + 1>{});
+      const char* V = vstage(PfParity<P>{}) + h * DV * 16 + l32 * 16;
+      // A operand of slot i: K rows (k-step i / 2, tile i % 2), then V^T
+      // chunks (k-slot x / ET, d-tile x % ET)
+      auto rd = [&](int i) -> u32x4 {
+        if (i < NQK) return *(const u32x4*)(K + k_rd[i >> 1] + (i & 1) * 32 * RB);
+        const int x = i - NQK;
+        return *(const u32x4*)(V + (x / ET) * 2 * DV * 16 + (x % ET) * 512);
+      };
+      const float mu = m == -INFINITY ? 0.f : m;           // rows with nothing visible yet
+      const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
       u32x4 pop[4];
-      qk(kstage(PfParity<P + 1>{}), sb0, sb1, piece);
-      numer(sa0, sa1, pop);
-      pv(vstage(PfParity<P>{}), pop);
+      float lb[4];
+      // P_j k-slot ks = 2^(s c - m) rounded to f16, packed as the B operand
+      // of the PV product (keys of S^T output registers 8 (ks % 2) .. + 8 of
+      // tile ks / 2); its row sum is taken over the rounded weights
+      auto ex = [&](int ks) {
+        lb[ks] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j0 = (ks & 1) * 8 + 2 * i;
+          const float x0 = ks < 2 ? sa0[j0] : sa1[j0];
+          const float x1 = ks < 2 ? sa0[j0 + 1] : sa1[j0 + 1];
+          const float p0 = fast_exp2(__builtin_fmaf(x0, a.qk_scale, -mu));
+          const float p1 = fast_exp2(__builtin_fmaf(x1, a.qk_scale, -mu));
+          const uint32_t w = pack2(F16{}, p0, p1);
+          lb[ks] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, lb[ks], false);
+          pop[ks][i] = w;
+        }
+      };
+      u32x4 buf[PD + 1];
+#pragma unroll
+      for (int i = 0; i < PD; ++i) buf[i] = rd(i);
+      sb0 = f32x16{};
+      sb1 = f32x16{};
+      ex(0);
+      ex(1);
+      ex(2);
+#pragma unroll
+      for (int i = 0; i < NS; ++i) {
+        if (i + PD < NS) buf[(i + PD) % (PD + 1)] = rd(i + PD);
+        const u32x4 av = buf[i % (PD + 1)];
+        if (i < NQK) {
+          if ((i & 1) == 0) sb0 = mfma32x32x16(T{}, av, qop[i >> 1], sb0);
+          else sb1 = mfma32x32x16(T{}, av, qop[i >> 1], sb1);
+          if (i & 1) {
+#pragma unroll
+            for (int p = 0; p < NP; ++p)
+              if ((p * KST) / NP == (i >> 1)) piece(p);
+          }
+        } else {
+          const int x = i - NQK;
+          o[x % ET] = mfma32x32x16(F16{}, av, pop[x / ET], o[x % ET]);
+        }
+        if (i == NQK - 1) ex(3);
+      }
+      l += (lb[0] + lb[1]) + (lb[2] + lb[3]);
       // the next block's row max (unmasked; redone below on masked blocks)
-      // shares this scheduling region, so its VALU fills the PV MFMA slots
       rmax = rowmax(sb0, sb1);
-      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);   // 4 K operand reads ahead
+      // slot pattern: two reads ahead, then per slot one MFMA, the read two
+      // slots on, the ring transfers after this k-step (QK slots), and the
+      // VALU work: exponentials (transcendental unit) and the other VALU
+      // instructions counted apart.  24 exponentials of P_j (k-slots 0-2)
+      // and their 48 fma/pack/row-sum instructions go under the QK slots, 8
+      // (k-slot 3) and 16 under the first half of the PV slots, the row max
+      // (~23 instructions) under the rest.
+      constexpr int TQ = (24 + NQK - 1) / NQK, VQ = (48 + NQK - 1) / NQK;
+      constexpr int TP = (8 + 2 * ET - 1) / (2 * ET), VP1 = (16 + 2 * ET - 1) / (2 * ET);
+      constexpr int VP2 = (24 + 2 * ET - 1) / (2 * ET);
+      __builtin_amdgcn_sched_group_barrier(0x100, PD, 0);
 #pragma unroll
-      for (int i = 0; i < 2 * KST; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one S MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // next operand read
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // softmax VALU
-        if (kInlineRefill && i % 2 == 1) {
+      for (int i = 0; i < NS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i + PD < NS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (kInlineRefill && i < NQK && (i & 1)) {
 #pragma unroll
-          for (int p = 0; p < NP; ++p)                        // the ring transfers after this k-step
-            if ((p * KST) / NP == i / 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+          for (int p = 0; p < NP; ++p)
+            if ((p * KST) / NP == (i >> 1)) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+        if (i < NQK) {
+          __builtin_amdgcn_sched_group_barrier(0x400, TQ, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, VQ, 0);
+        } else if (i < NQK + 2 * ET) {
+          __builtin_amdgcn_sched_group_barrier(0x400, TP, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, VP1, 0);
+        } else {
+          __builtin_amdgcn_sched_group_barrier(0x002, VP2, 0);
         }
       }
-#pragma unroll
-      for (int i = 0; i < 4 * ET; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one PV MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);   // softmax / row-max VALU
-      }
-      if (j + 1 >= wfull) {
+      // (keeps the row sum inside this scheduling region: otherwise it sinks
+      // below the branch that follows, where nothing overlaps it)
+      asm volatile("" : "+v"(l));
+      // (the scores of block wblk are discarded: no mask for them)
+      if (j + 1 >= wfull && j + 1 < wblk) {
         mask(sb0, sb1, (j + 1) * kPfBN);
         rmax = rowmax(sb0, sb1);
       }
@@ -669,7 +715,7 @@ void prefill_fwd(const PrefillArgs a) {
     // barrier.
     auto super = [&](auto parity, int j, bool second) {
       constexpr int P = decltype(parity)::value;          // 0 or 2
-      wait_vmcnt(0);                                      // this wave's DMA of blocks j, j+1 landed
+      wait_vmcnt<0>();                                      // this wave's DMA of blocks j, j+1 landed
       ring_barrier();                                     // everyone's landed; blocks j-2, j-1 retired
       // refills: K_{j+3}, V_{j+2} from block j's QK, K_{j+4}, V_{j+3} from
       // block j+1's (all into stages retired at this barrier)
@@ -689,21 +735,25 @@ void prefill_fwd(const PrefillArgs a) {
         for (int p = 0; p < NP; ++p) piece1(p);
       }
     };
+    // Prologue: K_0's transfers first, then q (its 32 rows per load
+    // instruction take the memory pipeline a while), then V_0, K_1, K_2,
+    // V_1.  The first scores wait for K_0 and q only; the rest land under
+    // them.  (Loads retire in order, so vmcnt(later) covers exactly K_0 and
+    // q.)
     if (nblk > 0) {
       issue_k(0, lk0);
+      load_q();
+      __builtin_amdgcn_sched_barrier(0);
       issue_v(0, lv0);
       issue_k(1, lk1);
       issue_k(2, lk2);
       issue_v(1, lv1);
-      if constexpr (ROPE != kRopeNone) {
-        // under the transfers' latency; nothing of the rotation (which waits
-        // for q) may be scheduled above the transfers
-        __builtin_amdgcn_sched_barrier(0);
-        rope_q_apply<D, T, ROPE>(a, qop, rq, h);
-      }
-      wait_vmcnt(0);
+      wait_vmcnt<2 * NK + 2 * NV>();
+      if constexpr (ROPE != kRopeNone) rope_q_apply<D, T, ROPE>(a, qop, rq, h);
       ring_barrier();
       first_scores();
+    } else {
+      load_q();
     }
     int j = 0;
     for (; j + 3 < nblk; j += 4) {
@@ -718,25 +768,26 @@ void prefill_fwd(const PrefillArgs a) {
     // K_{j+2} and V_{j+1}.
     auto step = [&](auto parity, int j, f32x16& sa0, f32x16& sa1, f32x16& sb0, f32x16& sb1) {
       constexpr int P = decltype(parity)::value;
-      wait_vmcnt(0);                                      // this wave's part of K_{j+1}, V_j landed
+      wait_vmcnt<0>();                                      // this wave's part of K_{j+1}, V_j landed
       ring_barrier();
       issue_k(j + 2, kstage(PfParity<P>{}));             // K_{j+2}, V_{j+1} into the stages retired here
       issue_v(j + 1, vstage(PfParity<P + 1>{}));
       work(parity, j, sa0, sa1, sb0, sb1, rmax, no_piece);
     };
+    // Prologue as on the four-stage ring: K_0, q, then V_0 and K_1 landing
+    // under the first scores.
     if (nblk > 0) {
       issue_k(0, lk0);
+      load_q();
+      __builtin_amdgcn_sched_barrier(0);
       issue_v(0, lv0);
       issue_k(1, lk1);
-      if constexpr (ROPE != kRopeNone) {
-        // under the transfers' latency; nothing of the rotation (which waits
-        // for q) may be scheduled above the transfers
-        __builtin_amdgcn_sched_barrier(0);
-        rope_q_apply<D, T, ROPE>(a, qop, rq, h);
-      }
-      wait_vmcnt(0);
+      wait_vmcnt<NK + NV>();
+      if constexpr (ROPE != kRopeNone) rope_q_apply<D, T, ROPE>(a, qop, rq, h);
       ring_barrier();
       first_scores();
+    } else {
+      load_q();
     }
     int j = 0;
     for (; j + 1 < nblk; j += 2) {
@@ -749,7 +800,7 @@ void prefill_fwd(const PrefillArgs a) {
   // ---- normalise and store.  The lane owns query qi, d = 32 e + 8 (j / 4) +
   // 4 h + j % 4 of O^T; the wave's 32 x D tile goes through LDS (16-byte
   // chunks swizzled by row) so that every global store writes whole rows.
-  wait_vmcnt(0);                                         // every ring transfer (empty ones fill zeros) landed
+  wait_vmcnt<0>();                                         // every ring transfer (empty ones fill zeros) landed
   ring_barrier();                                        // every wave is done with the ring
   {
     constexpr int NCH = D / 8;                           // 16-byte chunks per row
@@ -773,7 +824,7 @@ void prefill_fwd(const PrefillArgs a) {
     for (int i = 0; i < 32 / RPI; ++i) {
       const int row = i * RPI + lane / NCH;
       const u32x4 w = *(const u32x4*)(tile + row * RB + ((c ^ (row % NCH)) * 16));
-      const int qrow = q0 + wave * 32 + row;
+      const int qrow = q0 + rg * 32 + row;
       if (qrow < a.Tq)
         *(u32x4*)(a.out + b * a.o_sb + (int64_t)hq * a.o_sh + (int64_t)qrow * a.o_sm + c * 16) = w;
     }

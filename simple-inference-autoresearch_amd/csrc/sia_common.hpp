@@ -133,6 +133,27 @@ __device__ __forceinline__ uint64_t uniform64(uint64_t x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Division by a divisor fixed for the whole launch, as a multiply-high and a
+// shift (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, the round-up method with an N + 1-bit
+// multiplier): with l = ceil(log2 d) and m = floor(2^32 (2^l - d) / d) + 1,
+// x / d = (umulhi(x, m) + x) >> l for 0 <= x < 2^32; the sum fits 32 bits
+// because callers keep x < 2^31.  The scalar unit does it in three
+// instructions instead of the ~25 dependent ones of a runtime division.
+struct FastDiv {
+  uint32_t m;
+  uint32_t l;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while (l < 32 && (1ull << l) < d) ++l;
+  const uint64_t m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return FastDiv{(uint32_t)m, l};
+}
+__device__ __forceinline__ int fdiv(int x, FastDiv f) {
+  return (int)((__umulhi((uint32_t)x, f.m) + (uint32_t)x) >> f.l);
+}
+
 // One rotary-embedding pair: oa = xa c - xb s, ob = xb c + xa s in fp32 with
 // every product and sum rounded on its own.  hipcc contracts a*b - c*d into
 // an FMA by default (and __fmul_rn is a plain multiply in this toolchain), so
