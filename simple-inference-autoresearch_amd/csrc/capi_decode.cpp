@@ -199,8 +199,9 @@ int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decod
     L.begin_event = (hipEvent_t)opts->main_begin_event;
     L.end_event = (hipEvent_t)opts->main_end_event;
   }
-  // the work line (B x tiles x unit blocks) is indexed with 32-bit integers
-  if ((int64_t)g.B * ((L.a.cap_tokens + kTile - 1) / kTile) * g.UB > 0x7fffffffLL)
+  // the work line (B x (tiles + the split's segment charge, at most 4) x unit
+  // blocks) is indexed with 32-bit integers
+  if ((int64_t)g.B * ((L.a.cap_tokens + kTile - 1) / kTile + 4) * g.UB > 0x7fffffffLL)
     return fail(SIA_ERR_UNSUPPORTED, "batch x cache capacity too large (more than 2^31 tiles of work)");
   const size_t pb = plan_bytes(g.B);
   const size_t ib = item_bytes(g);

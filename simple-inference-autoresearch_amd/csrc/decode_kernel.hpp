@@ -45,7 +45,7 @@ constexpr int kTile = 16;          // tokens per MFMA tile
 // for decode_reduce: total work W (tiles x unit blocks), the number G of
 // work-groups that share it, the unit blocks per sequence; the work prefix
 // per sequence (B+1 ints) follows.
-constexpr int kPlanW = 0, kPlanG = 1, kPlanUB = 2, kPlanHeader = 4;
+constexpr int kPlanW = 0, kPlanG = 1, kPlanUB = 2, kPlanPen = 3, kPlanHeader = 4;
 constexpr int kMinGroupTiles = 8;  // least work per work-group, in tiles
 // The running max is only raised when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^8: well inside f16/bf16 range, and the
@@ -68,6 +68,7 @@ struct DecodeArgs {
   float qk_scale;                                    // sm_scale * log2(e)
   float* ws_acc; float* ws_ml; int32_t* ws_plan; int32_t max_items; int32_t G16;
   int32_t tps_force;
+  int32_t seg_pen;                                   // virtual tiles charged to each segment start (the split)
   int32_t slots;                                     // persistent work-groups of decode_main
   int32_t scale_vec;                                 // scale rows allow 16-byte vector loads
   // 32-bit copies of the per-tile strides (bytes): page strides (0 when
@@ -93,48 +94,19 @@ __device__ __forceinline__ int seq_tokens(const DecodeArgs& a, int b) {
   return n < 0 ? 0 : (n > a.cap_tokens ? a.cap_tokens : n);
 }
 
-// Block-wide reductions over NW waves (red: LDS scratch of >= 2*NW ints).
+// Exclusive scan over the sequences of their work (tiles + pen per nonempty
+// sequence, times UB unit blocks) into pre[0..B] (pre[B] = total), in LDS;
+// pre[b] holds sequence b's tile count on entry.
 template <int NW>
-__device__ __forceinline__ void block_sum_max(long long& sum, int& mx, int* red) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int s_lo = (int)sum;  // per-thread partials stay < 2^31 (tiles * units per thread)
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    s_lo += __shfl_xor(s_lo, o);
-    mx = max(mx, __shfl_xor(mx, o));
-  }
-  __syncthreads();
-  if (lane == 0) { red[wave] = s_lo; red[NW + wave] = mx; }
-  __syncthreads();
-  long long t = 0; int m = 0;
-#pragma unroll
-  for (int w = 0; w < NW; ++w) { t += red[w]; m = max(m, red[NW + w]); }
-  sum = t; mx = m;
-}
-
-// ceil(n / t) for 0 <= n < 2^31, t >= 1, given rt = 1.0 / t in double
-// precision: the product is within one of n / t, and one correction step
-// each way makes the floor exact (integer division is a long instruction
-// sequence on the GPU).
-__device__ __forceinline__ int ceil_div(int n, int t, double rt) {
-  int q = (int)((double)n * rt);
-  int r = n - q * t;
-  q += (r >= t) - (r < 0);
-  r = n - q * t;
-  return q + (r > 0);
-}
-
-// Exclusive scan of cnt[0..B) into pre[0..B] (pre[B] = total), in LDS.
-template <int NW>
-__device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pre, int* red, int UB) {
+__device__ __forceinline__ void block_scan(const DecodeArgs& a, int* pre, int* red, int UB, int pen) {
   const int T = NW * 64, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int per = (a.B + T - 1) / T;
   const int b0 = tid * per;
-  const double rt = 1.0 / tps;
+  auto work = [&](int nt) { return (nt + (nt > 0 ? pen : 0)) * UB; };
   int local = 0;
   for (int i = 0; i < per; ++i) {
     int b = b0 + i;
-    if (b < a.B) local += ceil_div(pre[b], tps, rt) * UB;
+    if (b < a.B) local += work(pre[b]);
   }
   int incl = local;
 #pragma unroll
@@ -153,43 +125,54 @@ __device__ __forceinline__ void block_scan(const DecodeArgs& a, int tps, int* pr
     if (b < a.B) {
       const int cnt = pre[b];
       pre[b] = run;
-      run += ceil_div(cnt, tps, rt) * UB;
+      run += work(cnt);
     }
   }
   if (tid == T - 1) pre[a.B] = run;
   __syncthreads();
 }
 
-// Decide tiles-per-split from the device-side lengths and build the item
-// prefix (items of sequence b are pre[b] .. pre[b+1]-1, split-major).
-//
-// Items are taken round-robin by the `gridDim.x` persistent work-groups, so a
-// split of t tiles finishes in about ceil(items / slots) * (t + overhead).
-// Thread c evaluates "split the longest sequence c+1 ways" and the cheapest
-// candidate wins (ties go to the larger split, i.e. fewer partials).  With
-// equal lengths this finds the exact balance; with ragged lengths it keeps
-// the heaviest slot close to the mean.
 // The work line of one call: sequence-major, then unit block, then 16-token
-// tile; pre[b] = position of sequence b's first tile (pre[B] = W).  One
-// length for the whole batch has a closed form; per-sequence lengths take a
-// block-wide scan.
+// tile; pre[b] = position of sequence b's first tile (pre[B] = W).  Every
+// segment (sequence, unit block) is charged `pen` virtual tiles ahead of its
+// tiles (the cost of starting it), so that the equal shares of the split also
+// even out the work-groups whose share holds more segment starts.  With equal
+// lengths the shares stay aligned to sequence boundaries without the charge,
+// and a charge would only move work between the groups of a sequence: there
+// pen is 0.  One length for the whole batch has a closed form; per-sequence
+// lengths take a block-wide min/max and scan.
 template <int NW>
-__device__ int plan_work(const DecodeArgs& a, int* pre, int* red, int tok0) {
+__device__ int plan_work(const DecodeArgs& a, int* pre, int* red, int tok0, int& pen) {
   const int T = NW * 64;
   if (!a.kv_per_seq) {
+    pen = 0;
     const int per = ((tok0 + kTile - 1) / kTile) * a.UB;
     for (int b = threadIdx.x; b <= a.B; b += T) pre[b] = b * per;
     __syncthreads();
     return a.B * per;
   }
   int* lens = pre + a.B + 1;                 // token counts, kept for the segments (small batches)
+  int nmin = 0x7fffffff, nmax = -1;
   for (int b = threadIdx.x; b < a.B; b += T) {
     const int n = seq_tokens(a, b);
-    pre[b] = (n + kTile - 1) / kTile;
+    const int nt = (n + kTile - 1) / kTile;
+    pre[b] = nt;
+    nmin = min(nmin, nt);
+    nmax = max(nmax, nt);
     if (a.B <= kLensInLds) lens[b] = n;
   }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    nmin = min(nmin, __shfl_xor(nmin, o));
+    nmax = max(nmax, __shfl_xor(nmax, o));
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) { red[wave] = nmin; red[NW + wave] = nmax; }
   __syncthreads();
-  block_scan<NW>(a, 1, pre, red, a.UB);
+#pragma unroll
+  for (int w = 0; w < NW; ++w) { nmin = min(nmin, red[w]); nmax = max(nmax, red[NW + w]); }
+  pen = nmin == nmax ? 0 : a.seg_pen;
+  block_scan<NW>(a, pre, red, a.UB, pen);
   return pre[a.B];
 }
 
@@ -626,7 +609,8 @@ void decode_main(const DecodeArgs a) {
   // together whatever the lengths, with no queue or atomics.  Group 0 records
   // the split for decode_reduce.
   const int tok0 = a.kv_per_seq ? 0 : uniform(seq_tokens(a, 0));
-  const int W = plan_work<NW>(a, pre, red, tok0);
+  int pen = 0;
+  const int W = plan_work<NW>(a, pre, red, tok0, pen);
   int G = (int)gridDim.x;
   if (a.tps_force > 0) G = min(G, max(1, (W + a.tps_force - 1) / a.tps_force));   // forced share (tests)
   G = min(G, max(1, (W + kMinGroupTiles - 1) / kMinGroupTiles));
@@ -637,6 +621,7 @@ void decode_main(const DecodeArgs a) {
       a.ws_plan[kPlanW] = W;
       a.ws_plan[kPlanG] = G;
       a.ws_plan[kPlanUB] = a.UB;
+      a.ws_plan[kPlanPen] = pen;
     }
   }
   const int g = blockIdx.x;
@@ -671,11 +656,20 @@ void decode_main(const DecodeArgs a) {
     // in LDS by the plan for batches up to kLensInLds, else are read again)
     const int ntok = a.kv_per_seq ? uniform(a.B <= kLensInLds ? pre[a.B + 1 + b] : seq_tokens(a, b)) : tok0;
     const int ntile = (ntok + kTile - 1) / kTile;
+    // the line holds each segment as pen virtual tiles (the cost of
+    // starting it: a few dependent memory round trips) followed by its ntile
+    // tiles; a piece of the virtual span maps to real tiles [t_lo, t_hi)
+    const int nvt = ntile + pen;
     const int rem = uniform(x - pre[b]);
-    const int ublk = rem / ntile;
-    const int t_lo = rem - ublk * ntile;
-    const int seg_end = min(x_hi, pre[b] + (ublk + 1) * ntile);
-    const int t_hi = t_lo + (seg_end - x);
+    const int ublk = rem / nvt;
+    const int r_lo = rem - ublk * nvt;
+    const int seg_end = min(x_hi, pre[b] + (ublk + 1) * nvt);
+    const int r_hi = r_lo + (seg_end - x);
+    const int t_lo = max(0, r_lo - pen), t_hi = max(0, r_hi - pen);
+    if (t_hi == t_lo) {        // only the start cost of a segment, at the end of the share
+      x = seg_end;
+      continue;
+    }
     const bool direct = t_lo == 0 && t_hi == ntile;
     const int pslot_id = first_seg ? 2 * g : 2 * g + 1;
     const int unit = ublk * shape.units + uin;
@@ -911,26 +905,29 @@ __global__ __launch_bounds__(kRedWaves * 64) void decode_reduce(const DecodeArgs
   const int b = (inr ? row : 0) / a.Hq;
   const int hq = (inr ? row : 0) - b * a.Hq;
   const int pb = a.ws_plan[kPlanHeader + b], pe = a.ws_plan[kPlanHeader + b + 1];
-  const int W = a.ws_plan[kPlanW], G = a.ws_plan[kPlanG];
+  const int W = a.ws_plan[kPlanW], G = a.ws_plan[kPlanG], pen = a.ws_plan[kPlanPen];
   // pieces of this row's (sequence, unit block): one per work-group in
   // [gf, gf + nsplit); the first group's piece is its first segment (slot
   // 2g) only if the range starts exactly at the group's start
   int nsplit = 1, gf = 0, s_first = 0, uin = 0, cc = 0;
   if (inr) {
-    const int ntile = (pe - pb) / a.UB;
+    const int nvt = (pe - pb) / a.UB;                // virtual tiles per unit block (0: empty sequence)
     const int hkv = hq / a.G, gi = hq - hkv * a.G;
     cc = gi & 15;
     const int unit = hkv * a.HG + (gi >> 4);
     const ItemShape shape = item_shape<NW>(a.U);
     const int ublk = unit / shape.units;
     uin = unit - ublk * shape.units;
-    if (ntile == 0) {
+    if (nvt == 0) {
       nsplit = 0;                                   // empty sequence: zeros
     } else {
-      const int x0 = pb + ublk * ntile;
-      gf = sk_group(x0, W, G);
-      nsplit = sk_group(x0 + ntile - 1, W, G) - gf + 1;
-      s_first = x0 != sk_lo(gf, W, G) ? 1 : 0;
+      // the segment spans virtual [v0, v0 + nvt); its tiles are the part
+      // after the first pen positions, held by groups gf .. (pieces); the
+      // piece of gf is that group's first segment unless gf started before v0
+      const int v0 = pb + ublk * nvt;
+      gf = sk_group(v0 + pen, W, G);
+      nsplit = sk_group(v0 + nvt - 1, W, G) - gf + 1;
+      s_first = sk_lo(gf, W, G) < v0 ? 1 : 0;
     }
   }
   const bool work = inr && nsplit != 1;

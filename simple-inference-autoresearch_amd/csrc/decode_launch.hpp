@@ -42,6 +42,12 @@ int launch_decode_typed(DecodeLaunch& L) {
   auto kmain = decode_main<D, KV, QT, ST, NW, false>;
   if constexpr (std::is_same<KV, I8>::value && std::is_same<ST, F32>::value)
     if (L.a.scale_vec) kmain = decode_main<D, KV, QT, ST, NW, true>;
+  // The split charges every segment start this many virtual tiles: starting
+  // a segment costs about four dependent memory round trips (its length and
+  // query, its first page id, its first tile), about two tiles of streaming
+  // time for 16-bit K/V and three for int8.  Equal lengths keep their shares
+  // aligned to sequence boundaries whatever the charge.
+  L.a.seg_pen = std::is_same<KV, I8>::value ? 3 : 2;
   const size_t lds = decode_lds_bytes(D, L.a.G16, L.a.B, NW);
   const int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
   if (occ <= 0) return fail(SIA_ERR_LAUNCH, "decode kernel does not fit on a CU (LDS %zu B)", lds);
