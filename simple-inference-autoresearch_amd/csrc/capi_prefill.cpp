@@ -169,15 +169,23 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.Tq = (int)Tq; a.Tk = (int)Tk;
   a.causal = causal != 0;
   a.qk_scale = sm_scale * 1.4426950408889634f;
-  const int bm = pf_rows_per_group((int)D);
-  a.nqblk = (int)((Tq + bm - 1) / bm);
+  // a work-group: hpw query heads of one KV head x 32 * waves / hpw rows each
+  const int hpw = pf_heads_per_group((int)D, a.G);
+  int lg = 0;
+  while ((1 << lg) < hpw) ++lg;
+  a.hpw_lg = lg;
+  const int rows = 32 * pf_waves((int)D) / hpw;
+  a.nqblk = (int)((Tq + rows - 1) / rows);
   a.nkb = (int)((Tk + kPfBN - 1) / kPfBN);
-  const int64_t groups = (int64_t)a.nqblk * B * Hkv;   // work-groups come in runs of G sharing a KV head
-  if (groups * a.G > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "grid too large");
-  a.remap = groups % 8 == 0;
-  a.dG = make_fastdiv((uint32_t)a.G);
+  const int64_t nunit = B * Hkv * (a.G / hpw);
+  if ((int64_t)a.nqblk * nunit > 0x7fffffff || B * Hkv > 0x7fffffff)
+    return fail(SIA_ERR_UNSUPPORTED, "grid too large");
+  a.nunit = (int)nunit;
+  a.remap = nunit % 8 == 0;
+  a.dU = make_fastdiv((uint32_t)nunit);
+  a.dU8 = make_fastdiv((uint32_t)(a.remap ? nunit / 8 : 1));
+  a.dBH = make_fastdiv((uint32_t)(B * Hkv));
   a.dHkv = make_fastdiv((uint32_t)Hkv);
-  a.dB = make_fastdiv((uint32_t)B);
   if (rope != nullptr && (rc = setup_rope(*rope, B, Tq, D, q->dtype, a))) return rc;
 
   PackArgs& p = L.pack;

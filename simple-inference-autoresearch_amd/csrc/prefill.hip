@@ -13,7 +13,7 @@ static int launch_prefill_typed(PrefillLaunch& L) {
     // one work-group per 64-key V^T image
     hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)L.pack.nblocks), dim3(256), 0, L.stream, L.pack);
   }
-  const int nwg = L.a.nqblk * L.a.B * L.a.Hq;
+  const int nwg = L.a.nqblk * L.a.nunit;
   const dim3 grid(nwg), block(PfCfg<D>::waves * 64);
   switch (rope) {
     case kRopeNone: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeNone>), grid, block, 0, L.stream, L.a); break;

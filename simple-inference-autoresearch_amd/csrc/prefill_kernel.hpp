@@ -15,8 +15,11 @@
 //    one 64-key block per image, laid out exactly as the main kernel's LDS
 //    wants it, so no work-group converts or transposes V again (each V block
 //    is read by every query block and every query head of its KV head).
-//  * A work-group of prefill_fwd is 8 waves x 32 query rows (BM = 256) of one
-//    (b, hq), two waves per SIMD.  It walks key blocks of BN = 64 through a
+//  * A work-group of prefill_fwd is 8 waves (two per SIMD) of 32 query rows
+//    each: the same rows of hpw query heads that share one KV head, 32 *
+//    8 / hpw rows per head (hpw = 4 at G = 4: 64 rows x 4 heads).  Every
+//    wave of a causal work-group then sees the same key blocks, so no wave
+//    idles while the last one finishes.  It walks key blocks of BN = 64 through a
 //    four-stage LDS ring per tensor filled by buffer_load ... lds (global ->
 //    LDS DMA, no VGPR staging): three blocks are in flight while one is
 //    computed, every wait is a constant vmcnt, and the per-step barrier
@@ -34,7 +37,7 @@
 //    PV MFMAs follow; the loop is unrolled by four so stage arrays and score
 //    registers are fixed per step at compile time.
 //  * Blocks are issued heaviest-first (the causal diagonal makes late query
-//    blocks the longest), and the query heads that share a KV head are placed
+//    blocks the longest), and every work-group of one (b, KV head) is placed
 //    on the same XCD so their K/V tiles are served by one L2.
 #pragma once
 
@@ -60,10 +63,12 @@ struct PrefillArgs {
   char* out; int64_t o_sb, o_sh, o_sm;
   int32_t B, Hq, Hkv, G, Tq, Tk, causal;
   float qk_scale;                               // sm_scale * log2(e)
-  int32_t nqblk;                                // ceil(Tq / 128)
+  int32_t nqblk;                                // ceil(Tq / rows per head per work-group)
   int32_t nkb;                                  // ceil(Tk / 64)
-  int32_t remap;                                // XCD-aware block order
-  FastDiv dG, dHkv, dB;                         // divisions by G, Hkv, B for the block mapping
+  int32_t hpw_lg;                               // log2 of the query heads per work-group (hpw)
+  int32_t nunit;                                // work-groups per query block: B * Hkv * (G / hpw)
+  int32_t remap;                                // XCD-aware block order (nunit % 8 == 0)
+  FastDiv dU, dU8, dBH, dHkv;                   // divisions by nunit, nunit / 8, B * Hkv, Hkv
   // rotary embedding of q at load (prefill_fwd<D, T, true> only): query row
   // i of sequence b sits at position start_host + start_pos[b or 0] + i
   // (start_pos NULL: 0) and is rotated by row pos of the cos/sin tables
@@ -94,7 +99,6 @@ struct PfCfg {
   static constexpr int waves = D <= 128 ? 8 : 4;
   static constexpr int stages = D <= 128 ? 4 : 2;
   static constexpr int wpe = D <= 128 ? 2 : 1;          // waves per SIMD the registers are budgeted for
-  static constexpr int BM = 32 * waves;                  // query rows per work-group
   static constexpr int DV = D < 32 ? 32 : D;             // V^T image dimensions
   static constexpr int kblk = kPfBN * D * 2;             // bytes of one K block
   static constexpr int vblk = kPfBN * DV * 2;            // bytes of one V^T image
@@ -105,8 +109,15 @@ struct PfCfg {
   static constexpr bool dummy = kper * waves != kdma || vper * waves != vdma;
 };
 
-// Query rows per work-group of prefill_fwd at head_dim D (host side).
-inline int pf_rows_per_group(int D) { return D <= 128 ? 256 : 128; }
+// Waves per work-group of prefill_fwd at head_dim D (host side).
+inline int pf_waves(int D) { return D <= 128 ? 8 : 4; }
+// Query heads per work-group: the largest power of two that divides the GQA
+// group size G and is at most the wave count (host side).
+inline int pf_heads_per_group(int D, int G) {
+  int h = 1;
+  while (2 * h <= pf_waves(D) && G % (2 * h) == 0) h *= 2;
+  return h;
+}
 
 // Key (0..63 within its block) held by element i (0..7) of image chunk c: the
 // keys of 16-key group c/2 in the order of the S^T output registers of lanes
@@ -352,7 +363,7 @@ template <int D, class T, int ROPE>
 __global__ __launch_bounds__(PfCfg<D>::waves * 64) __attribute__((amdgpu_waves_per_eu(PfCfg<D>::wpe)))
 void prefill_fwd(const PrefillArgs a) {
   using C = PfCfg<D>;
-  constexpr int NW = C::waves, S = C::stages, DV = C::DV, BM = C::BM;
+  constexpr int NW = C::waves, S = C::stages, DV = C::DV;
   constexpr int KST = D / 16;                   // QK k-steps
   constexpr int ET = DV / 32;                   // O^T d-tiles
   constexpr int KB = C::kblk, VB = C::vblk;
@@ -375,32 +386,43 @@ void prefill_fwd(const PrefillArgs a) {
     return I == 0 ? lv0 : I == 1 ? lv1 : I == 2 ? lv2 : lv3;
   };
 
-  // ---- block -> (query block, b, hq), heaviest first, KV-head groups per XCD
-  int lin = blockIdx.x;
-  if (a.remap) {
-    const int xcd = lin & 7, slot = lin >> 3;
-    const int sg = fdiv(slot, a.dG);
-    lin = (sg * 8 + xcd) * a.G + (slot - sg * a.G);
+  // ---- block -> (query block, unit), heaviest first.  A unit is (b, KV
+  // head, group of hpw query heads); u = hgrp * B * Hkv + b * Hkv + hkv, so
+  // with the XCD-aware order (block index % 8 = XCD) every unit of one (b,
+  // KV head) lands on one XCD when B * Hkv % 8 == 0.
+  int ql, u;
+  {
+    const int lin = blockIdx.x;
+    if (a.remap) {
+      const int xcd = lin & 7, slot = lin >> 3;
+      ql = fdiv(slot, a.dU8);
+      u = xcd + 8 * (slot - ql * (a.nunit >> 3));
+    } else {
+      ql = fdiv(lin, a.dU);
+      u = lin - ql * a.nunit;
+    }
   }
-  int rest = fdiv(lin, a.dG);
-  const int g = lin - rest * a.G;
-  const int r2 = fdiv(rest, a.dHkv);
-  const int hkv = rest - r2 * a.Hkv;
-  const int r3 = fdiv(r2, a.dB);
-  const int b = r2 - r3 * a.B;
-  const int qblk = a.nqblk - 1 - r3;
-  const int hq = hkv * a.G + g;
-
+  const int bhn = a.B * a.Hkv;
+  const int hgrp = fdiv(u, a.dBH);
+  const int bh = u - hgrp * bhn;
+  const int b = fdiv(bh, a.dHkv);
+  const int hkv = bh - b * a.Hkv;
+  const int qblk = a.nqblk - 1 - ql;
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int l32 = lane & 31, h = lane >> 5;
   const int off = a.Tk - a.Tq;                           // bottom-right causal offset
-  const int q0 = qblk * BM;
-  // The 32-row group of the work-group's rows this wave owns.  Waves w and
-  // w + 4 share a SIMD; under a causal mask later row groups see more key
-  // blocks, so the second wave of each SIMD takes the groups in reverse
-  // (7, 6, 5, 4) and every SIMD carries the same number of key blocks.
-  const int rg = PfCfg<D>::wpe == 2 && wave >= NW / 2 ? 3 * NW / 2 - 1 - wave : wave;
+  // This wave's head (wave % hpw) and 32-row group (wave / hpw) of the
+  // work-group's rpg = NW / hpw row groups per head.  Waves w and w + 4 share
+  // a SIMD; under a causal mask later row groups see more key blocks, so with
+  // several row groups the second wave of each SIMD takes them in reverse
+  // and every SIMD carries the same number of key blocks.
+  const int rpg = NW >> a.hpw_lg;
+  const int hw = wave & ((1 << a.hpw_lg) - 1);
+  const int r0 = wave >> a.hpw_lg;
+  const int rg = PfCfg<D>::wpe == 2 && wave >= NW / 2 && rpg > 1 ? rpg - 1 - (r0 - rpg / 2) : r0;
+  const int hq = hkv * a.G + (hgrp << a.hpw_lg) + hw;
+  const int q0 = qblk * 32 * rpg;                        // the work-group's first row (every head)
   const int qi = q0 + rg * 32 + l32;                     // this lane's query row
 
   // ---- Q^T operand (B of S^T = K Q^T): query qi, d = 16 j + 8 h + [0, 8)
@@ -417,7 +439,7 @@ void prefill_fwd(const PrefillArgs a) {
     }
   };
 
-  const int kend = a.causal ? min(a.Tk, off + q0 + BM) : a.Tk;
+  const int kend = a.causal ? min(a.Tk, off + q0 + 32 * rpg) : a.Tk;
   const int nblk = kend > 0 ? (kend + kPfBN - 1) / kPfBN : 0;   // key blocks of the work-group
   const int wrow0 = q0 + rg * 32;                        // this wave's first row
   const int wend = a.causal ? min(a.Tk, off + wrow0 + 32) : a.Tk;   // keys this wave can see
