@@ -100,6 +100,21 @@ def test_strided_views_and_token_major(gpu_pkg):
     check(ref_layout, O.flash_attention(f64(q), f64(k), f64(v), True), "strided")
 
 
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 4), (12, 4), (6, 1), (8, 1), (32, 2), (24, 2)])
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("B,causal", [(1, True), (3, False), (2, True)])
+def test_head_groupings(gpu_pkg, Hq, Hkv, D, B, causal):
+    """Work-groups span the query heads of one KV head (powers of two dividing G):
+    MHA, G = 2, 3, 4, 6, 8, 12 and 16, one or several head groups per KV head,
+    batches whose unit count is or is not a multiple of 8 (XCD-aware order or not)."""
+    announce(f"prefill heads {Hq}/{Hkv} D={D} B={B} causal={causal}")
+    Tq, Tk = (130, 130) if causal else (97, 230)
+    q, k, v = qkv(B, Hq, Hkv, Tq, Tk, D, torch.bfloat16, seed=Hq * 31 + Hkv * 7 + D + B)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    check(out, O.flash_attention(f64(q), f64(k), f64(v), causal), f"{Hq}/{Hkv} D={D} B={B}")
+
+
 def test_gqa_mapping(gpu_pkg):
     """Each query head reads KV head hq // G: give each KV head a constant V."""
     announce("prefill GQA mapping")
