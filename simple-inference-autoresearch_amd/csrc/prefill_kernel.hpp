@@ -763,17 +763,54 @@ void prefill_fwd(const PrefillArgs a) {
     // them.  (Loads retire in order, so vmcnt(later) covers exactly K_0 and
     // q.)
     if (nblk > 0) {
-      issue_k(0, lk0);
-      load_q();
-      __builtin_amdgcn_sched_barrier(0);
-      issue_v(0, lv0);
-      issue_k(1, lk1);
-      issue_k(2, lk2);
-      issue_v(1, lv1);
-      wait_vmcnt<2 * NK + 2 * NV>();
-      if constexpr (ROPE != kRopeNone) rope_q_apply<D, T, ROPE>(a, qop, rq, h);
-      ring_barrier();
-      first_scores();
+      if constexpr (ROPE == kRopeNone) {
+        // q comes through LDS: each wave's 32 rows by 1 KB LDS DMA (whole
+        // rows, swizzled like the K stages) into a stage the first blocks do
+        // not use yet (V_1's, K_3's, V_2's, V_3's; 2 waves each), then read in
+        // the operand layout.  Loaded straight into registers, each of a
+        // wave's q instructions touched 32 rows (256 cache-line requests per
+        // wave instead of 64), and the memory pipeline worked through them
+        // ahead of the ring's first transfers.  Rows past Tq read as zeros.
+        issue_k(0, lk0);
+        issue_v(0, lv0);
+        issue_k(1, lk1);
+        issue_k(2, lk2);
+        char* qst = ((wave >> 1) == 0 ? lv1 : (wave >> 1) == 1 ? lk3 : (wave >> 1) == 2 ? lv2 : lv3) +
+                    (wave & 1) * 32 * RB;
+        {
+          const int r0w = q0 + rg * 32;
+          const int nrow = max(0, min(32, a.Tq - r0w));
+          const int bytes = nrow > 0 ? (nrow - 1) * (int)a.q_sm + RB : 0;
+          const __amdgpu_buffer_rsrc_t rsq = __builtin_amdgcn_make_buffer_rsrc(
+              (void*)(a.q + b * a.q_sb + (int64_t)hq * a.q_sh + (int64_t)min(r0w, a.Tq - 1) * a.q_sm), 0, bytes,
+              kBufferFlags);
+#pragma unroll
+          for (int i = 0; i < 32 * RB / 1024; ++i) {
+            const int r = i * ROWS_PER_DMA + lane / NC;
+            const int voff = r * (int)a.q_sm + (((lane % NC) ^ (r % NC)) * 16);
+            char* dst = qst + i * 1024;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsq, dst, 16, voff, 0, 0, 0);
+          }
+        }
+        wait_vmcnt<0>();                                  // this wave's q (and K_0 .. K_2, V_0) landed
+#pragma unroll
+        for (int j = 0; j < KST; ++j) qop[j] = *(const u32x4*)(qst + k_rd[j]);
+        ring_barrier();                                   // every wave's q read and K_0 landed
+        issue_v(1, lv1);                                  // into the q stage just read
+        first_scores();
+      } else {
+        issue_k(0, lk0);
+        load_q();
+        __builtin_amdgcn_sched_barrier(0);
+        issue_v(0, lv0);
+        issue_k(1, lk1);
+        issue_k(2, lk2);
+        issue_v(1, lv1);
+        wait_vmcnt<2 * NK + 2 * NV>();
+        rope_q_apply<D, T, ROPE>(a, qop, rq, h);
+        ring_barrier();
+        first_scores();
+      }
     } else {
       load_q();
     }
