@@ -390,17 +390,18 @@ void prefill_fwd(const PrefillArgs a) {
   // head, group of hpw query heads); u = hgrp * B * Hkv + b * Hkv + hkv, so
   // with the XCD-aware order (block index % 8 = XCD) every unit of one (b,
   // KV head) lands on one XCD when B * Hkv % 8 == 0.
+  // (both orders computed and one selected: a branch here made the compiler
+  // load the kernel arguments in four dependent rounds instead of two)
   int ql, u;
   {
     const int lin = blockIdx.x;
-    if (a.remap) {
-      const int xcd = lin & 7, slot = lin >> 3;
-      ql = fdiv(slot, a.dU8);
-      u = xcd + 8 * (slot - ql * (a.nunit >> 3));
-    } else {
-      ql = fdiv(lin, a.dU);
-      u = lin - ql * a.nunit;
-    }
+    const int xcd = lin & 7, slot = lin >> 3;
+    const int ql8 = fdiv(slot, a.dU8);
+    const int u8 = xcd + 8 * (slot - ql8 * (a.nunit >> 3));
+    const int ql1 = fdiv(lin, a.dU);
+    const int u1 = lin - ql1 * a.nunit;
+    ql = a.remap ? ql8 : ql1;
+    u = a.remap ? u8 : u1;
   }
   const int bhn = a.B * a.Hkv;
   const int hgrp = fdiv(u, a.dBH);
