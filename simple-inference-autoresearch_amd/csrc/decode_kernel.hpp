@@ -171,7 +171,10 @@ __device__ int plan_work(const DecodeArgs& a, int* pre, int* red, int tok0, int&
   __syncthreads();
 #pragma unroll
   for (int w = 0; w < NW; ++w) { nmin = min(nmin, red[w]); nmax = max(nmax, red[NW + w]); }
-  pen = nmin == nmax ? 0 : a.seg_pen;
+  // (read from LDS, so the compiler cannot tell it is the same in every
+  // lane: without readfirstlane the tile descriptors derived from it would be
+  // taken as divergent and every tile load wrapped in a waterfall loop)
+  pen = uniform(nmin == nmax ? 0 : a.seg_pen);
   block_scan<NW>(a, pre, red, a.UB, pen);
   return pre[a.B];
 }
