@@ -88,16 +88,22 @@ struct PackArgs {
 constexpr int kPfBN = 64;               // keys per block
 constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (32-bit data, no swizzle)
 
-// Per-head-dim configuration of prefill_fwd.  Up to D = 128: 8 waves (two per
-// SIMD, 256 VGPRs each), a four-stage K/V ring (three blocks in flight).
-// D = 256: the O^T accumulators alone take 128 registers per lane, so 4 waves
-// run one per SIMD with 512 registers, and the 32 KB blocks fit LDS as a
-// two-stage ring.  The PV product works on 32-dimension tiles, so V images are
-// at least 32 dimensions wide (D = 16 is zero-padded).
+// Per-head-dim configuration of prefill_fwd.
+//  * D = 128: 8 waves (two per SIMD, 256 VGPRs each) and a four-stage K/V ring
+//    (three blocks in flight); one work-group (128 KB of LDS) per CU.
+//  * D <= 64: 4 waves with the same register budget, so two work-groups share
+//    a CU and one's prologue and epilogue overlap the other's key loop (MHA
+//    D = 64 at T = 1024: 88 -> 70 us per call); a two-stage ring at D = 64,
+//    four stages below, where blocks are small (measured best of the two).
+//  * D = 256: the O^T accumulators alone take 128 registers per lane, so 4
+//    waves run one per SIMD with 512 registers, and the 32 KB blocks fit LDS
+//    as a two-stage ring.
+// The PV product works on 32-dimension tiles, so V images are at least 32
+// dimensions wide (D = 16 is zero-padded).
 template <int D>
 struct PfCfg {
-  static constexpr int waves = D <= 128 ? 8 : 4;
-  static constexpr int stages = D <= 128 ? 4 : 2;
+  static constexpr int waves = D == 128 ? 8 : 4;
+  static constexpr int stages = D == 128 || D < 64 ? 4 : 2;
   static constexpr int wpe = D <= 128 ? 2 : 1;          // waves per SIMD the registers are budgeted for
   static constexpr int DV = D < 32 ? 32 : D;             // V^T image dimensions
   static constexpr int kblk = kPfBN * D * 2;             // bytes of one K block
@@ -110,7 +116,7 @@ struct PfCfg {
 };
 
 // Waves per work-group of prefill_fwd at head_dim D (host side).
-inline int pf_waves(int D) { return D <= 128 ? 8 : 4; }
+inline int pf_waves(int D) { return D == 128 ? 8 : 4; }
 // Query heads per work-group: the largest power of two that divides the GQA
 // group size G and is at most the wave count (host side).
 inline int pf_heads_per_group(int D, int G) {
@@ -414,14 +420,14 @@ void prefill_fwd(const PrefillArgs a) {
   const int l32 = lane & 31, h = lane >> 5;
   const int off = a.Tk - a.Tq;                           // bottom-right causal offset
   // This wave's head (wave % hpw) and 32-row group (wave / hpw) of the
-  // work-group's rpg = NW / hpw row groups per head.  Waves w and w + 4 share
-  // a SIMD; under a causal mask later row groups see more key blocks, so with
-  // several row groups the second wave of each SIMD takes them in reverse
-  // and every SIMD carries the same number of key blocks.
+  // work-group's rpg = NW / hpw row groups per head.  With 8 waves, waves w
+  // and w + 4 share a SIMD; under a causal mask later row groups see more key
+  // blocks, so with several row groups the second wave of each SIMD takes
+  // them in reverse and every SIMD carries the same number of key blocks.
   const int rpg = NW >> a.hpw_lg;
   const int hw = wave & ((1 << a.hpw_lg) - 1);
   const int r0 = wave >> a.hpw_lg;
-  const int rg = PfCfg<D>::wpe == 2 && wave >= NW / 2 && rpg > 1 ? rpg - 1 - (r0 - rpg / 2) : r0;
+  const int rg = NW == 8 && wave >= NW / 2 && rpg > 1 ? rpg - 1 - (r0 - rpg / 2) : r0;
   const int hq = hkv * a.G + (hgrp << a.hpw_lg) + hw;
   const int q0 = qblk * 32 * rpg;                        // the work-group's first row (every head)
   const int qi = q0 + rg * 32 + l32;                     // this lane's query row
