@@ -171,9 +171,13 @@ int prepare_scales(const sia_tensor* ks, const sia_tensor* vs, const sia_tensor*
     a.ks_pg = (uint32_t)a.ks_s0; a.vs_pg = (uint32_t)a.vs_s0;
   }
   L.scale_dtype = ks->dtype;
-  a.scale_vec = ks->dtype == SIA_F32 && ks->stride[2] == 1 && vs->stride[2] == 1 && aligned16(ks->data) &&
-                aligned16(vs->data) && bstride(ks, 0) % 16 == 0 && bstride(ks, 1) % 16 == 0 &&
-                bstride(vs, 0) % 16 == 0 && bstride(vs, 1) % 16 == 0;
+  // the 4 scales a lane reads per tile form one aligned vector (16 bytes of
+  // fp32, 8 of fp16) when the rows are contiguous and every row start is
+  // aligned to that size
+  const int64_t al = ks->dtype == SIA_F32 ? 16 : 8;
+  a.scale_vec = ks->stride[2] == 1 && vs->stride[2] == 1 && (uintptr_t)ks->data % al == 0 &&
+                (uintptr_t)vs->data % al == 0 && bstride(ks, 0) % al == 0 && bstride(ks, 1) % al == 0 &&
+                bstride(vs, 0) % al == 0 && bstride(vs, 1) % al == 0;
   return SIA_OK;
 }
 

@@ -70,7 +70,7 @@ struct DecodeArgs {
   int32_t tps_force;
   int32_t seg_pen;                                   // virtual tiles charged to each segment start (the split)
   int32_t slots;                                     // persistent work-groups of decode_main
-  int32_t scale_vec;                                 // scale rows allow 16-byte vector loads
+  int32_t scale_vec;                                 // scale rows allow one vector load per lane
   // 32-bit copies of the per-tile strides (bytes): page strides (0 when
   // contiguous) and token strides, so the tile address needs only 32x32->64
   // products
@@ -267,7 +267,8 @@ __device__ __forceinline__ float load_scale(__amdgpu_buffer_rsrc_t rs, uint32_t 
 
 // Load this lane's operands of one tile.  FULL: all 16 tokens exist, so no
 // per-lane predicate; otherwise tokens >= `valid` read as zero.  SV: the
-// int8 scales of a head are contiguous fp32 rows (one 16-byte load per lane);
+// int8 scales of a head are contiguous rows (one 16-byte load per lane for
+// fp32 scales, one 8-byte load for fp16);
 // a compile-time choice, so that the tile loop holds no branch around loads
 // (a branch there makes the compiler wait for the next tile's loads as well).
 template <int D, class KV, class ST, bool FULL, bool SV>
@@ -284,12 +285,19 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, const TilePtr& t,
   }
   if constexpr (C::kInt8) {
     const __amdgpu_buffer_rsrc_t rks = tile_rsrc(t.ks), rvs = tile_rsrc(t.vs);
-    if constexpr (FULL && SV) {
-      static_assert(std::is_same<ST, F32>::value, "vector scale loads are fp32");
+    if constexpr (FULL && SV && std::is_same<ST, F32>::value) {
       const u32x4 k4 = __builtin_amdgcn_raw_buffer_load_b128(rks, o.ks, 0, kLoadNT);
       const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(rvs, o.vs, 0, kLoadNT);
 #pragma unroll
       for (int i = 0; i < 4; ++i) { c.ks[i] = __uint_as_float(k4[i]); c.vs[i] = __uint_as_float(v4[i]); }
+    } else if constexpr (FULL && SV) {   // fp16 scale rows: the 4 scales in one 8-byte load
+      const u32x2 k2 = __builtin_amdgcn_raw_buffer_load_b64(rks, o.ks, 0, kLoadNT);
+      const u32x2 v2 = __builtin_amdgcn_raw_buffer_load_b64(rvs, o.vs, 0, kLoadNT);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c.ks[i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(k2[i >> 1] >> (16 * (i & 1))));
+        c.vs[i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(v2[i >> 1] >> (16 * (i & 1))));
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -572,9 +580,11 @@ __device__ __forceinline__ int out_d(int g, int i, int e) {
 
 // Waves per SIMD each instantiation is compiled for (its VGPR budget).  A
 // work-group is NW = 8 waves, so below 4 waves per SIMD a CU holds one group.
+// int8 at D = 64 gets 256 registers too: its int8 query split, scales and
+// conversions do not fit 128 without scratch spills.
 template <int D, class KV>
 struct DecodeWaves {
-  static constexpr int value = D <= 64 ? 4 : (D <= 128 ? 2 : 1);
+  static constexpr int value = D <= 64 && !std::is_same<KV, I8>::value ? 4 : (D <= 128 ? 2 : 1);
 };
 
 // Geometry of one item inside a work-group of NW waves (all uniform).

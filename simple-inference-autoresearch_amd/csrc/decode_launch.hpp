@@ -37,10 +37,11 @@ inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {
 template <int D, class KV, class QT, class ST>
 int launch_decode_typed(DecodeLaunch& L) {
   constexpr int NW = decode_waves(D);
-  // int8 K/V with fp32 scale rows: one 16-byte scale load per lane when the
-  // rows allow it (decided on the host, compiled as two kernels)
+  // int8 K/V: one vector scale load per lane (16 bytes of fp32 or 8 of fp16
+  // scales) when the scale rows allow it (decided on the host, compiled as
+  // two kernels)
   auto kmain = decode_main<D, KV, QT, ST, NW, false>;
-  if constexpr (std::is_same<KV, I8>::value && std::is_same<ST, F32>::value)
+  if constexpr (std::is_same<KV, I8>::value)
     if (L.a.scale_vec) kmain = decode_main<D, KV, QT, ST, NW, true>;
   // The split charges every segment start this many virtual tiles: starting
   // a segment costs about four dependent memory round trips (its length and

@@ -99,6 +99,38 @@ def test_contiguous_int8(gpu_pkg, q_dtype, scale_dtype, D):
         assert_close(out, ref, 2e-3, "int8 (tight)")
 
 
+@pytest.mark.parametrize("scale_dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_int8_scale_row_layouts(gpu_pkg, scale_dtype, D):
+    """Scale rows that allow one vector load per lane (contiguous, aligned) and
+    ones that do not (rows starting one element in; every other token of a
+    wider row) read the same scales: bit-identical outputs, and the oracle's."""
+    announce(f"int8 decode scale layouts D={D} scales={scale_dtype}")
+    B, Hq, Hkv, S = 3, 8, 2, 300
+    q, ki, vi, ks, vs = contiguous_case(B, Hq, Hkv, S, D, torch.int8, torch.bfloat16, seed=11,
+                                        scale_dtype=scale_dtype)
+    lens = [300, 1, 129]
+    kl = torch.tensor(lens, dtype=torch.int32, device=DEV)
+    base = gpu_pkg.attention_flash_decode_int8(q, ki, vi, ks, vs, kl)
+
+    def offset_by_one(s):
+        w = torch.zeros(B, Hkv, S + 1, dtype=s.dtype, device=DEV)
+        w[..., 1:] = s
+        return w[..., 1:]
+
+    def every_other(s):
+        w = torch.zeros(B, Hkv, 2 * S, dtype=s.dtype, device=DEV)
+        w[..., ::2] = s
+        return w[..., ::2]
+
+    for f in (offset_by_one, every_other):
+        out = gpu_pkg.attention_flash_decode_int8(q, ki, vi, f(ks), f(vs), kl)
+        torch.cuda.synchronize()
+        assert torch.equal(out, base), f.__name__
+    ref = O.int8_decode(f64(q), ki.cpu().numpy(), vi.cpu().numpy(), f64(ks), f64(vs), lens)
+    assert_close(base, ref, 2e-3, "int8 scale layouts")
+
+
 def test_shared_scalar_kv_len_and_cache_views(gpu_pkg):
     """Reference call pattern: k/v are [layer, :B] views of an (L,B,Hkv,S,D) pool."""
     announce("cache-view decode")
