@@ -46,7 +46,7 @@ constexpr int kTile = 16;          // tokens per MFMA tile
 // work-groups that share it, the unit blocks per sequence; the work prefix
 // per sequence (B+1 ints) follows.
 constexpr int kPlanW = 0, kPlanG = 1, kPlanUB = 2, kPlanPen = 3, kPlanHeader = 4;
-constexpr int kMinGroupTiles = 8;  // least work per work-group, in tiles
+constexpr int kMinGroupTiles = 4;  // least work per work-group, in tiles
 // The running max is only raised when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^8: well inside f16/bf16 range, and the
 // rescale of (l, acc) almost never runs after the first tile.
@@ -900,18 +900,22 @@ void decode_main(const DecodeArgs a) {
 // are uniform over the wave (the largest piece count of its rows).  Rows of
 // sequences the main kernel wrote directly are skipped; empty sequences are
 // written as zeros.
+//
+// PW waves share a work-group's rows: wave w merges the w-th of PW
+// contiguous runs of the pieces, and wave 0 merges the PW states through
+// LDS.  PW = 1 when the rows fill the GPU by themselves; a small batch (few
+// rows, each split over up to a few hundred work-groups) uses PW = 8, which
+// cuts a row's chain of dependent round trips by 8.
 constexpr int kRedBatch = 16;
-// Waves per work-group of decode_reduce: one, so that the few hundred rows
-// of a small batch spread over every CU instead of a quarter of them.
-constexpr int kRedWaves = 1;
 
-template <int D, class OT, int NW>
-__global__ __launch_bounds__(kRedWaves * 64) void decode_reduce(const DecodeArgs a) {
+template <int D, class OT, int NW, int PW>
+__global__ __launch_bounds__(PW * 64) void decode_reduce(const DecodeArgs a) {
   constexpr int LPR = D / 4;          // lanes per row
-  constexpr int RPW = 64 / LPR;       // rows per wave
+  constexpr int RPW = 64 / LPR;       // rows per work-group
   const int lane = threadIdx.x & 63;
+  const int wave = PW > 1 ? uniform(threadIdx.x >> 6) : 0;
   const int li = lane % LPR;
-  const int row = (blockIdx.x * kRedWaves + (threadIdx.x >> 6)) * RPW + lane / LPR;
+  const int row = blockIdx.x * RPW + lane / LPR;
   const bool inr = row < a.B * a.Hq;
   // the plan's header and this row's prefix entries in one round trip
   // (loaded before any test of them, for rows past the end as well)
@@ -947,23 +951,30 @@ __global__ __launch_bounds__(kRedWaves * 64) void decode_reduce(const DecodeArgs
   int nmax = work ? nsplit : 0;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) nmax = max(nmax, __shfl_xor(nmax, o));
+  // (the same rows in every wave: the whole work-group leaves together)
   if (!__any(work)) return;   // (wave-uniform) nothing to merge or zero here
   auto slot = [&](int s) {
     const int id = 2 * (gf + s) + (s == 0 ? s_first : 0);
     return ((int64_t)id * NW + uin) * a.G16 + cc;
   };
+  // this wave's run of pieces [sb, se) (uniform); a lane merges those below
+  // its own count
+  const int chunk = (nmax + PW - 1) / PW;
+  const int sb = min(nmax, wave * chunk), se = min(nmax, sb + chunk);
+  const int lim = min(nsplit, se);
   float M = -INFINITY, L = 0.f;
   f32x4 A = {0.f, 0.f, 0.f, 0.f};
-  // Merge pieces [s0, s0 + K).  Every load is issued: a piece past the row's
-  // count reads the row's first piece and a lane with no merge to do reads
-  // slot 0 (one address per instruction), and both are masked once loaded.
+  // Merge pieces [s0, s0 + K) below lim.  Every load is issued: a piece at
+  // or past lim reads the row's first piece and a lane with no merge to do
+  // reads slot 0 (one address per instruction), and both are masked once
+  // loaded.
   auto batch = [&](int s0, auto kk) {
     constexpr int K = decltype(kk)::value;
     float m[K], l[K];
     f32x4 x[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const int64_t sl = work ? slot(s0 + k < nsplit ? s0 + k : 0) : 0;
+      const int64_t sl = work ? slot(s0 + k < lim ? s0 + k : 0) : 0;
       const float2 ml = *(const float2*)(a.ws_ml + sl * 2);
       m[k] = ml.x;
       l[k] = ml.y;
@@ -973,7 +984,7 @@ __global__ __launch_bounds__(kRedWaves * 64) void decode_reduce(const DecodeArgs
     float mb = M;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      if (!(work && s0 + k < nsplit)) m[k] = -INFINITY;
+      if (!(work && s0 + k < lim)) m[k] = -INFINITY;
       mb = fmaxf(mb, m[k]);
     }
     // branch-free, so that no load is moved behind a test of the maxima:
@@ -990,12 +1001,35 @@ __global__ __launch_bounds__(kRedWaves * 64) void decode_reduce(const DecodeArgs
     }
     M = mb;
   };
-  for (int s0 = 0; s0 < nmax; s0 += kRedBatch) {
-    const int rem = nmax - s0;   // wave-uniform
+  for (int s0 = sb; s0 < se; s0 += kRedBatch) {
+    const int rem = se - s0;   // wave-uniform
     if (rem <= 2) batch(s0, std::integral_constant<int, 2>{});
     else if (rem <= 4) batch(s0, std::integral_constant<int, 4>{});
     else if (rem <= 8) batch(s0, std::integral_constant<int, 8>{});
     else batch(s0, std::integral_constant<int, kRedBatch>{});
+  }
+  if constexpr (PW > 1) {
+    // states of waves 1 .. PW-1, merged by wave 0 (an empty run is M = -inf,
+    // L = 0, A = 0 and weighs out)
+    __shared__ f32x4 s_a[PW - 1][64];
+    __shared__ float s_m[PW - 1][64], s_l[PW - 1][64];
+    if (wave > 0) {
+      s_a[wave - 1][lane] = A;
+      s_m[wave - 1][lane] = M;
+      s_l[wave - 1][lane] = L;
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < PW - 1; ++w) {
+      const float mw = s_m[w][lane];
+      const float mb = fmaxf(M, mw);
+      const float mref = mb == -INFINITY ? 0.f : mb;
+      const float r0 = fast_exp2(M - mref), r1 = fast_exp2(mw - mref);
+      L = L * r0 + s_l[w][lane] * r1;
+      A = A * r0 + s_a[w][lane] * r1;
+      M = mb;
+    }
   }
   if (!work) return;
   const float inv = 1.0f / (L == 0.f ? 1.f : L);

@@ -62,9 +62,13 @@ int launch_decode_typed(DecodeLaunch& L) {
   if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
   const int rows = L.a.B * L.a.Hq;
-  constexpr int kRowsPerGroup = kRedWaves * (64 / (D / 4));   // 64 / (D/4) rows per wave
-  hipLaunchKernelGGL((decode_reduce<D, QT, NW>), dim3((rows + kRowsPerGroup - 1) / kRowsPerGroup),
-                     dim3(kRedWaves * 64), 0, L.stream, L.a);
+  constexpr int kRowsPerGroup = 64 / (D / 4);
+  const int ngroups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
+  // rows too few to fill the CUs: 8 waves split each row's pieces
+  if (ngroups < device_info().cus)
+    hipLaunchKernelGGL((decode_reduce<D, QT, NW, 8>), dim3(ngroups), dim3(8 * 64), 0, L.stream, L.a);
+  else
+    hipLaunchKernelGGL((decode_reduce<D, QT, NW, 1>), dim3(ngroups), dim3(64), 0, L.stream, L.a);
   e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode reduce launch: %s", hipGetErrorString(e));
   return SIA_OK;

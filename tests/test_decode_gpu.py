@@ -99,6 +99,28 @@ def test_contiguous_int8(gpu_pkg, q_dtype, scale_dtype, D):
         assert_close(out, ref, 2e-3, "int8 (tight)")
 
 
+@pytest.mark.parametrize("kv", ["bf16", "int8"])
+@pytest.mark.parametrize("n", [32768, 5000])
+def test_single_sequence_long_context(gpu_pkg, kv, n):
+    """One sequence: the split spreads it over every work-group (hundreds of
+    pieces per output row), merged by the reduce whose waves split a row's
+    pieces."""
+    announce(f"single-sequence decode {kv} n={n}")
+    B, Hq, Hkv, D = 1, 32, 8, 128
+    kvd = torch.int8 if kv == "int8" else torch.bfloat16
+    q, k, v, ks, vs = contiguous_case(B, Hq, Hkv, n, D, kvd, torch.bfloat16, seed=n % 97,
+                                      scale_dtype=torch.float16)
+    kl = torch.tensor([n], dtype=torch.int32, device=DEV)
+    if kv == "int8":
+        out = gpu_pkg.gqa_int8_flash_decode(q, k, v, ks, vs, kl)
+        ref = O.int8_decode(f64(q), k.cpu().numpy(), v.cpu().numpy(), f64(ks), f64(vs), [n])
+    else:
+        out = gpu_pkg.attention_flash_decode(q, k, v, kl)
+        ref = O.gqa_decode(f64(q), f64(k), f64(v), [n])
+    torch.cuda.synchronize()
+    assert_close(out, ref, 2e-3, f"{kv} n={n}")
+
+
 @pytest.mark.parametrize("scale_dtype", [torch.float32, torch.float16])
 @pytest.mark.parametrize("D", [64, 128])
 def test_int8_scale_row_layouts(gpu_pkg, scale_dtype, D):
