@@ -169,12 +169,21 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.Tq = (int)Tq; a.Tk = (int)Tk;
   a.causal = causal != 0;
   a.qk_scale = sm_scale * 1.4426950408889634f;
-  // a work-group: hpw query heads of one KV head x 32 * waves / hpw rows each
-  const int hpw = pf_heads_per_group((int)D, a.G);
+  // a work-group: hpw query heads of one KV head x 32 * waves / hpw rows each.
+  // At D = 128, a grid of at most one 8-wave group per CU runs as 4-wave
+  // groups instead (prefill_fwd variant 1): twice the groups, each with half
+  // the rows.  (Up to two 8-wave groups per CU this was measured slower.)
+  auto groups = [&](int var) {
+    const int h = pf_heads_per_group((int)D, a.G, var);
+    const int64_t r = 32 * pf_waves((int)D, var) / h;
+    return ((Tq + r - 1) / r) * (B * Hkv * (a.G / h));
+  };
+  L.var = D == 128 && groups(0) <= dev.cus ? 1 : 0;
+  const int hpw = pf_heads_per_group((int)D, a.G, L.var);
   int lg = 0;
   while ((1 << lg) < hpw) ++lg;
   a.hpw_lg = lg;
-  const int rows = 32 * pf_waves((int)D) / hpw;
+  const int rows = 32 * pf_waves((int)D, L.var) / hpw;
   a.nqblk = (int)((Tq + rows - 1) / rows);
   a.nkb = (int)((Tk + kPfBN - 1) / kPfBN);
   const int64_t nunit = B * Hkv * (a.G / hpw);

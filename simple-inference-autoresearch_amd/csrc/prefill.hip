@@ -5,6 +5,9 @@
 
 namespace sia {
 
+template <int D, class T, int VAR>
+static int launch_fwd(PrefillLaunch& L, int rope);
+
 template <int D, class T>
 static int launch_prefill_typed(PrefillLaunch& L) {
   // rotary variant: none, or split-half / interleaved pairs from 16-bit / fp32 tables
@@ -13,14 +16,21 @@ static int launch_prefill_typed(PrefillLaunch& L) {
     // one work-group per 64-key V^T image
     hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)L.pack.nblocks), dim3(256), 0, L.stream, L.pack);
   }
+  if constexpr (D == 128)
+    if (L.var == 1) return launch_fwd<D, T, 1>(L, rope);
+  return launch_fwd<D, T, 0>(L, rope);
+}
+
+template <int D, class T, int VAR>
+static int launch_fwd(PrefillLaunch& L, int rope) {
   const int nwg = L.a.nqblk * L.a.nunit;
-  const dim3 grid(nwg), block(PfCfg<D>::waves * 64);
+  const dim3 grid(nwg), block(PfCfg<D, VAR>::waves * 64);
   switch (rope) {
-    case kRopeNone: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeNone>), grid, block, 0, L.stream, L.a); break;
-    case kRopeSplit16: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeSplit16>), grid, block, 0, L.stream, L.a); break;
-    case kRopeInter16: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeInter16>), grid, block, 0, L.stream, L.a); break;
-    case kRopeSplit32: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeSplit32>), grid, block, 0, L.stream, L.a); break;
-    default: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeInter32>), grid, block, 0, L.stream, L.a); break;
+    case kRopeNone: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeNone, VAR>), grid, block, 0, L.stream, L.a); break;
+    case kRopeSplit16: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeSplit16, VAR>), grid, block, 0, L.stream, L.a); break;
+    case kRopeInter16: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeInter16, VAR>), grid, block, 0, L.stream, L.a); break;
+    case kRopeSplit32: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeSplit32, VAR>), grid, block, 0, L.stream, L.a); break;
+    default: hipLaunchKernelGGL((prefill_fwd<D, T, kRopeInter32, VAR>), grid, block, 0, L.stream, L.a); break;
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "prefill launch: %s", hipGetErrorString(e));

@@ -91,6 +91,10 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 // Per-head-dim configuration of prefill_fwd.
 //  * D = 128: 8 waves (two per SIMD, 256 VGPRs each) and a four-stage K/V ring
 //    (three blocks in flight); one work-group (128 KB of LDS) per CU.
+//    Variant 1 (VAR = 1, chosen by the host when the 8-wave grid would not
+//    exceed the CU count, e.g. one sequence of up to 2048 tokens): 4 waves
+//    and a two-stage ring, so twice the work-groups, and a causal work-group
+//    covers half the rows (B1 T = 1024: 30.5 -> 25.6 us per call).
 //  * D <= 64: 4 waves with the same register budget, so two work-groups share
 //    a CU and one's prologue and epilogue overlap the other's key loop (MHA
 //    D = 64 at T = 1024: 88 -> 70 us per call); a two-stage ring at D = 64,
@@ -100,10 +104,11 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 //    as a two-stage ring.
 // The PV product works on 32-dimension tiles, so V images are at least 32
 // dimensions wide (D = 16 is zero-padded).
-template <int D>
+template <int D, int VAR = 0>
 struct PfCfg {
-  static constexpr int waves = D == 128 ? 8 : 4;
-  static constexpr int stages = D == 128 || D < 64 ? 4 : 2;
+  static constexpr bool small = VAR == 1;
+  static constexpr int waves = D == 128 && !small ? 8 : 4;
+  static constexpr int stages = small ? 2 : D == 128 || D < 64 ? 4 : 2;
   static constexpr int wpe = D <= 128 ? 2 : 1;          // waves per SIMD the registers are budgeted for
   static constexpr int DV = D < 32 ? 32 : D;             // V^T image dimensions
   static constexpr int kblk = kPfBN * D * 2;             // bytes of one K block
@@ -116,12 +121,12 @@ struct PfCfg {
 };
 
 // Waves per work-group of prefill_fwd at head_dim D (host side).
-inline int pf_waves(int D) { return D == 128 ? 8 : 4; }
+inline int pf_waves(int D, int var = 0) { return D == 128 && var == 0 ? 8 : 4; }
 // Query heads per work-group: the largest power of two that divides the GQA
 // group size G and is at most the wave count (host side).
-inline int pf_heads_per_group(int D, int G) {
+inline int pf_heads_per_group(int D, int G, int var = 0) {
   int h = 1;
-  while (2 * h <= pf_waves(D) && G % (2 * h) == 0) h *= 2;
+  while (2 * h <= pf_waves(D, var) && G % (2 * h) == 0) h *= 2;
   return h;
 }
 
@@ -365,10 +370,14 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 
-template <int D, class T, int ROPE>
-__global__ __launch_bounds__(PfCfg<D>::waves * 64) __attribute__((amdgpu_waves_per_eu(PfCfg<D>::wpe)))
+// (one template argument each: __launch_bounds__ is a macro)
+template <int C> constexpr int kPfThreads = PfCfg<C / 2, C % 2>::waves * 64;
+template <int C> constexpr int kPfWpe = PfCfg<C / 2, C % 2>::wpe;
+
+template <int D, class T, int ROPE, int VAR>
+__global__ __launch_bounds__(kPfThreads<2 * D + VAR>) __attribute__((amdgpu_waves_per_eu(kPfWpe<2 * D + VAR>)))
 void prefill_fwd(const PrefillArgs a) {
-  using C = PfCfg<D>;
+  using C = PfCfg<D, VAR>;
   constexpr int NW = C::waves, S = C::stages, DV = C::DV;
   constexpr int KST = D / 16;                   // QK k-steps
   constexpr int ET = DV / 32;                   // O^T d-tiles

@@ -146,6 +146,25 @@ def test_cfg4_full_size(gpu_pkg):
     print(f"cfg4 max abs err on 4 heads: {worst:.3e}")
 
 
+@pytest.mark.parametrize("B,Tq,Tk,causal", [(2, 2100, 2100, True), (4, 600, 2500, True), (2, 1500, 1700, False)])
+def test_d128_grid_sizes(gpu_pkg, B, Tq, Tk, causal):
+    """head_dim 128 runs 8-wave work-groups when the grid of them exceeds the
+    CU count (these shapes; the small shapes of the other tests run 4-wave
+    groups): ragged and offset lengths against the oracle on a head subset."""
+    announce(f"prefill D=128 B={B} Tq={Tq} Tk={Tk} causal={causal}")
+    g = torch.Generator(device=DEV).manual_seed(Tq + Tk)
+    q = (torch.randn(B, 32, Tq, 128, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    k = (torch.randn(B, 8, Tk, 128, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    v = (torch.randn(B, 8, Tk, 128, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    for b, hq in ((0, 0), (B - 1, 13), (B // 2, 31)):
+        hkv = hq // 4
+        ref = O.flash_attention(f64(q[b:b + 1, hq:hq + 1]), f64(k[b:b + 1, hkv:hkv + 1]),
+                                f64(v[b:b + 1, hkv:hkv + 1]), causal)
+        check(out[b:b + 1, hq:hq + 1], ref, f"b={b} hq={hq}")
+
+
 def test_prefill_errors(gpu_pkg):
     announce("prefill errors")
     q, k, v = qkv(1, 4, 2, 8, 8, 128, torch.bfloat16, seed=1)
