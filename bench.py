@@ -13,8 +13,10 @@ the whole call (GB/s); ``roofline`` refers to the dominant kernel
 (``decode_main``), timed with HIP events recorded by the library on the launch
 stream around that kernel alone; ``cpu_baseline`` times the reference's CPU
 torch path (restated in ``oracle/eager_path.py``) on a bounded sample of the
-same workload.  ``other_configs`` carries configs 2 and 5 (decode) and 4
-(prefill) measured the same way when available.
+same workload.  ``other_configs`` carries configs 1, 2 and 5 (decode), 4
+(prefill), the fused RoPE, the Qwen3.5 shapes and one-sequence shapes
+(``small``: prefill at the reference benchmark's lengths, single-sequence
+decode) measured the same way when available.
 """
 
 from __future__ import annotations
@@ -461,6 +463,51 @@ def bench_qwen35_config(pkg, steps: int, warmup: int):
     return out
 
 
+def bench_small_config(pkg, steps: int, warmup: int):
+    """One sequence at a time (Llama-3.1-8B attention shapes: 32/8 heads, head_dim 128,
+    bf16): causal prefill at the reference's own benchmark lengths
+    (benchmarks/benchmark_kernel/bench_attention_compare.py:99-105, B1, T 128 .. 4096),
+    and decode over a contiguous cache of 8192 and 32768 tokens (bf16, and int8 with
+    the fp16 scales of the reference's KVCache)."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(13)
+    Hq, Hkv, D = 32, 8, 128
+    out = {}
+    for T in (128, 512, 1024, 2048, 4096):
+        q = (torch.randn(1, Hq, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        k = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        v = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+        t = time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True), steps, warmup)
+        flops = _syn().prefill_flops(1, Hq, T, D)
+        tf = flops / (t["mean_ms"] * 1e-3) / 1e12
+        out[f"prefill_B1_T{T}"] = {**_timing_fields(t), "TFLOPs_back_to_back": round(tf, 1),
+                                   "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+    q = torch.randn(1, Hq, 1, D, device=dev, generator=g).to(torch.bfloat16)
+    for S in (8192, 32768):
+        kv_len = torch.tensor([S], dtype=torch.int32, device=dev)
+        k = torch.randn(1, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+        v = torch.randn(1, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
+        t = time_calls(lambda: pkg.attention_flash_decode(q, k, v, kv_len), steps, warmup)
+        nbytes = 2 * Hkv * S * D * 2 + 2 * Hq * D * 2
+        gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
+        out[f"decode_bf16_B1_ctx{S}"] = {**_timing_fields(t), "GBps_back_to_back": round(gbs, 1),
+                                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+        ki = torch.randint(-127, 128, (1, Hkv, S, D), device=dev, generator=g, dtype=torch.int8)
+        vi = torch.randint(-127, 128, (1, Hkv, S, D), device=dev, generator=g, dtype=torch.int8)
+        ks = (torch.rand(1, Hkv, S, device=dev, generator=g) * 0.02 + 1e-3).to(torch.float16)
+        vs = (torch.rand(1, Hkv, S, device=dev, generator=g) * 0.02 + 1e-3).to(torch.float16)
+        t = time_calls(lambda: pkg.attention_flash_decode_int8(q, ki, vi, ks, vs, kv_len), steps, warmup)
+        nbytes = 2 * Hkv * S * (D + 2) + 2 * Hq * D * 2
+        gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
+        out[f"decode_int8_B1_ctx{S}"] = {**_timing_fields(t), "GBps_back_to_back": round(gbs, 1),
+                                         "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    out["workload"] = ("one sequence, 32/8 heads, head_dim 128, bf16: causal prefill at the reference "
+                       "benchmark's lengths; decode over a contiguous cache (rates from back-to-back calls)")
+    return out
+
+
 def bench_copy(steps: int, warmup: int, nbytes: int = 1 << 30):
     """A plain device-to-device copy of `nbytes` (torch's copy kernel).
 
@@ -506,7 +553,7 @@ def main(argv=None):
     p.add_argument("--settle-ms", type=float, default=300.0,
                    help="untimed back-to-back calls before each config's warm-up, so the GPU clocks settle")
     p.add_argument("--no-others", action="store_true", help="skip configs 2, 4, 5, the RoPE and the Qwen3.5 lines")
-    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "rope", "qwen35", "copy"],
+    p.add_argument("--config", default="cfg3", choices=["cfg2", "cfg3", "cfg4", "cfg5", "rope", "qwen35", "small", "copy"],
                    help="config to run alone (profiling runs); 'copy' is a plain 1 GiB device copy "
                         "that calibrates the HBM byte counters")
     args = p.parse_args(argv)
@@ -530,6 +577,10 @@ def main(argv=None):
     if args.config == "copy":   # counter calibration: 1 GiB read + 1 GiB written per launch
         r = bench_copy(args.steps, args.warmup)
         print(json.dumps({"config": "copy", **r}), flush=True)
+        return 0
+    if args.config == "small":   # one-sequence shapes only (profiling runs)
+        r = bench_small_config(pkg, args.steps, args.warmup)
+        print(json.dumps({"config": "small", **r}), flush=True)
         return 0
     if args.config == "qwen35":   # Qwen3.5 attention shapes only (profiling runs)
         r = bench_qwen35_config(pkg, args.steps, args.warmup)
@@ -619,6 +670,8 @@ def main(argv=None):
         print(f"[bench] rope: {others['rope']}", file=sys.stderr, flush=True)
         others["qwen35"] = bench_qwen35_config(pkg, max(50, args.steps // 2), args.warmup)
         print(f"[bench] qwen35: {others['qwen35']}", file=sys.stderr, flush=True)
+        others["small"] = bench_small_config(pkg, max(50, args.steps // 2), args.warmup)
+        print(f"[bench] small: {others['small']}", file=sys.stderr, flush=True)
         result["other_configs"] = others
         case = None
 
