@@ -20,7 +20,7 @@ namespace {
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
 struct Geometry {
-  int B, Hq, Hkv, D, G, HG, U, UB, G16;
+  int B, Hq, Hkv, D, G, HG, U, UB, IU, G16;
 };
 
 size_t plan_bytes(int B) { return (size_t)round_up((int64_t)(kPlanHeader + B + 1) * 4, 256); }
@@ -47,9 +47,31 @@ int geometry(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, Geometry& g) {
   g.HG = (g.G + 15) / 16;
   g.U = g.Hkv * g.HG;
   const int nw = decode_waves(g.D);
-  g.UB = g.U >= nw ? (g.U + nw - 1) / nw : 1;
+  g.IU = g.U < nw ? g.U : nw;   // units per item (see item_units)
+  g.UB = (g.U + g.IU - 1) / g.IU;
   g.G16 = g.G < 16 ? g.G : 16;
   return SIA_OK;
+}
+
+// Units per item (the work-group's unit of work: IU units, NW / IU waves
+// each).  IU starts at min(U, NW) and halves while the batch has fewer items
+// than CUs: smaller items give the split more, shorter pieces to share out,
+// and once there is an item per work-group every output row is written
+// directly, with nothing for the split-K merge.  A contiguous cache takes the
+// halved IU.  A paged pool takes it only when it reaches an item per CU (B64
+// x 8 KV heads: 2 units of 4 waves, config 3 182.5 -> 180.6 us per call):
+// a page holds every KV head's 16 tokens side by side, the waves of a wide
+// item read them together, and narrower items that still leave a split ran
+// config 2's main kernel 2-2.5 us (7%) slower.
+void item_units(Geometry& g, bool paged) {
+  const int nw = decode_waves(g.D);
+  const int cus = device_info().cus > 0 ? device_info().cus : 256;
+  auto items = [&](int iu) { return (int64_t)g.B * ((g.U + iu - 1) / iu); };
+  g.IU = g.U < nw ? g.U : nw;
+  int iu = g.IU;
+  while (iu % 2 == 0 && items(iu) < cus) iu /= 2;
+  if (!paged || items(iu) >= cus) g.IU = iu;
+  g.UB = (g.U + g.IU - 1) / g.IU;
 }
 
 int check_tensor(const sia_tensor* t, const char* name, int ndim) {
@@ -100,7 +122,7 @@ int prepare_common(const sia_tensor* q, const sia_tensor* kv_len, const sia_tens
   a.out = (char*)out->data; a.o_sb = bstride(out, 0); a.o_sh = bstride(out, 2);
   a.kv_len = (const int32_t*)kv_len->data;
   a.kv_per_seq = (n == g.B && g.B > 1) ? 1 : 0;
-  a.B = g.B; a.Hq = g.Hq; a.Hkv = g.Hkv; a.G = g.G; a.HG = g.HG; a.U = g.U; a.UB = g.UB; a.G16 = g.G16;
+  a.B = g.B; a.Hq = g.Hq; a.Hkv = g.Hkv; a.G = g.G; a.HG = g.HG; a.U = g.U; a.UB = g.UB; a.IU = g.IU; a.G16 = g.G16;
   a.qk_scale = sm_scale * 1.4426950408889634f;
   L.D = g.D;
   L.q_dtype = q->dtype;
@@ -310,6 +332,9 @@ int decode_any(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, co
   int rc;
   if (k == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "k is NULL");
   if ((rc = prepare_common(q, kv_len, out, (int)k->shape[1], sm_scale, g, L))) return rc;
+  item_units(g, bt != nullptr);
+  L.a.IU = g.IU;
+  L.a.UB = g.UB;
   if ((rc = prepare_kv(k, v, g, bt != nullptr, page_size, L))) return rc;
   if (want_int8) {
     if (k->dtype != SIA_I8) return fail(SIA_ERR_INVALID_ARGUMENT, "k/v must be int8 for the int8 entry points");

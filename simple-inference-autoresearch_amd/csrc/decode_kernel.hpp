@@ -18,10 +18,11 @@
 //    each group takes an equal contiguous share, cut into segments at
 //    (sequence, unit block) boundaries, so ragged batches stay balanced with
 //    no work queue.
-//  * Within a segment the group's NW wave64s cover NW units.  Its waves split the
-//    item's 16-token tiles (double-buffered in registers); each wave runs its
-//    own online softmax and the waves' (m, l, acc) states are merged through
-//    LDS.  A segment that covers its whole (sequence, unit block) is
+//  * Within a segment the group's NW wave64s cover the IU units of an item
+//    (IU chosen on the host, smaller for small batches), NW / IU waves per
+//    unit splitting its 16-token tiles (double-buffered in registers); each
+//    wave runs its own online softmax and the waves' (m, l, acc) states are
+//    merged through LDS.  A segment that covers its whole (sequence, unit block) is
 //    normalised and written straight to `out`; otherwise it writes an fp32
 //    partial and decode_reduce() merges the pieces.
 //  * Per tile a wave computes S^T = K Q^T with v_mfma_f32_16x16x32 (tokens as
@@ -46,7 +47,7 @@ constexpr int kTile = 16;          // tokens per MFMA tile
 // work-groups that share it, the unit blocks per sequence; the work prefix
 // per sequence (B+1 ints) follows.
 constexpr int kPlanW = 0, kPlanG = 1, kPlanUB = 2, kPlanPen = 3, kPlanHeader = 4;
-constexpr int kMinGroupTiles = 4;  // least work per work-group, in tiles
+constexpr int kMinWaveTiles = 2;   // least work per work-group: this many tiles per wave of a unit
 // The running max is only raised when a score exceeds it by more than this
 // (log2 units), so p = 2^(s - m) <= 2^8: well inside f16/bf16 range, and the
 // rescale of (l, acc) almost never runs after the first tile.
@@ -65,6 +66,7 @@ struct DecodeArgs {
   const int32_t* kv_len; int32_t kv_per_seq;
   int32_t cap_tokens;                                // S (contiguous) or max_blocks*page_size
   int32_t B, Hq, Hkv, G, HG, U, UB;                  // U = Hkv*HG units per sequence, UB unit blocks per item row
+  int32_t IU;                                        // units per item (NW / IU waves per unit)
   float qk_scale;                                    // sm_scale * log2(e)
   float* ws_acc; float* ws_ml; int32_t* ws_plan; int32_t max_items; int32_t G16;
   int32_t tps_force;
@@ -587,19 +589,19 @@ struct DecodeWaves {
   static constexpr int value = D <= 64 && !std::is_same<KV, I8>::value ? 4 : (D <= 128 ? 2 : 1);
 };
 
-// Geometry of one item inside a work-group of NW waves (all uniform).
-//   U >= NW: the item covers NW units (one per wave), phases P = 1.
-//   U <  NW: the item covers all U units; P = NW / U waves share a unit and
-//            split its tiles by phase (merged through LDS afterwards).
+// Geometry of one item inside a work-group of NW waves (all uniform): it
+// covers IU units (chosen on the host), and P = NW / IU waves share each unit
+// and split its tiles by phase (merged through LDS afterwards; P = 1 writes
+// from registers).
 struct ItemShape {
   int units;   // units covered by one item (<= NW)
   int P;       // waves per unit
 };
 template <int NW>
-__device__ __forceinline__ ItemShape item_shape(int U) {
+__device__ __forceinline__ ItemShape item_shape(const DecodeArgs& a) {
   ItemShape sh;
-  if (U >= NW) { sh.units = NW; sh.P = 1; }
-  else { sh.units = U; sh.P = NW / U; }
+  sh.units = a.IU;
+  sh.P = NW / a.IU;
   return sh;
 }
 
@@ -616,7 +618,7 @@ void decode_main(const DecodeArgs a) {
   int* red = (int*)(l_l + NW * a.G16);
   int* pre = red + 2 * NW + 2;
 
-  const ItemShape shape = item_shape<NW>(a.U);
+  const ItemShape shape = item_shape<NW>(a);
   // The work line (every work-group computes the same prefix) and its
   // stream-K split: group g takes an equal contiguous share, so groups finish
   // together whatever the lengths, with no queue or atomics.  Group 0 records
@@ -626,7 +628,7 @@ void decode_main(const DecodeArgs a) {
   const int W = plan_work<NW>(a, pre, red, tok0, pen);
   int G = (int)gridDim.x;
   if (a.tps_force > 0) G = min(G, max(1, (W + a.tps_force - 1) / a.tps_force));   // forced share (tests)
-  G = min(G, max(1, (W + kMinGroupTiles - 1) / kMinGroupTiles));
+  G = min(G, max(1, (W + kMinWaveTiles * shape.P - 1) / (kMinWaveTiles * shape.P)));
   G = min(G, max(1, a.max_items / 2));                      // two partial slots per group
   if (blockIdx.x == 0) {
     for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[kPlanHeader + i] = pre[i];
@@ -932,7 +934,7 @@ __global__ __launch_bounds__(PW * 64) void decode_reduce(const DecodeArgs a) {
     const int hkv = hq / a.G, gi = hq - hkv * a.G;
     cc = gi & 15;
     const int unit = hkv * a.HG + (gi >> 4);
-    const ItemShape shape = item_shape<NW>(a.U);
+    const ItemShape shape = item_shape<NW>(a);
     const int ublk = unit / shape.units;
     uin = unit - ublk * shape.units;
     if (nvt == 0) {
