@@ -1,0 +1,70 @@
+"""Seeded sweep of prefill shapes against the float64 oracle.
+
+Each case draws (head_dim, KV heads, GQA group, batch, query and key lengths,
+causal, dtype, output layout) from a fixed generator, so a failure names a
+case that reruns identically.  The draws span both work-group variants at
+head_dim 128 (grids below and above the CU count), chunked prefill (Tq < Tk)
+and Tq > Tk (leading rows see no key), one and several head groups per KV
+head.  Tolerance as in the other prefill tests: 2e-3, or one output ulp where
+|o| makes a single rounding larger.
+"""
+
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce
+from oracle import attention as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+N_CASES = 24
+
+
+def f64(t):
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def ulp(x, dtype):
+    mant = {torch.bfloat16: 7, torch.float16: 10}[dtype]
+    return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -24))) - mant)
+
+
+def draw(i: int) -> dict:
+    r = random.Random(5000 + i)
+    while True:
+        Tk = r.choice([1, 40, 64, 129, 300, 700, 1100])
+        shape = r.random()
+        Tq = Tk if shape < 0.5 else (r.randint(1, Tk) if shape < 0.8 else Tk + r.randint(1, 80))
+        c = dict(D=r.choice([16, 32, 64, 128, 128, 256]), Hkv=r.choice([1, 2, 4, 8]), G=r.choice([1, 2, 3, 4, 8]),
+                 B=r.choice([1, 2, 4]), Tq=Tq, Tk=Tk, causal=r.random() < 0.7,
+                 dtype=r.choice([torch.bfloat16, torch.float16]), token_major=r.random() < 0.3, seed=31 + i)
+        if c["B"] * c["Hkv"] * c["G"] * c["Tq"] * c["Tk"] * c["D"] <= 400_000_000:
+            return c
+
+
+@pytest.mark.parametrize("i", range(N_CASES))
+def test_random_prefill_shape(gpu_pkg, i):
+    c = draw(i)
+    announce(f"prefill sweep case {i}: D={c['D']} Hkv={c['Hkv']} G={c['G']} B={c['B']} Tq={c['Tq']} Tk={c['Tk']} "
+             f"causal={c['causal']} {c['dtype']}")
+    B, Hkv, D = c["B"], c["Hkv"], c["D"]
+    Hq = Hkv * c["G"]
+    g = torch.Generator(device=DEV).manual_seed(c["seed"])
+    q = (torch.randn(B, Hq, c["Tq"], D, generator=g, device=DEV) * 0.5).to(c["dtype"])
+    k = (torch.randn(B, Hkv, c["Tk"], D, generator=g, device=DEV) * 0.5).to(c["dtype"])
+    v = (torch.randn(B, Hkv, c["Tk"], D, generator=g, device=DEV) * 0.5).to(c["dtype"])
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=c["causal"], out_token_major=c["token_major"])
+    torch.cuda.synchronize()
+    if c["token_major"]:
+        out = out.transpose(1, 2)
+    ref = O.flash_attention(f64(q), f64(k), f64(v), c["causal"])
+    got = f64(out)
+    assert got.shape == ref.shape and np.isfinite(got).all()
+    err = np.abs(got - ref)
+    allowed = np.maximum(2e-3, ulp(ref, c["dtype"]))
+    assert (err <= allowed).all(), f"case {i} {c}: max err {err.max():.3e}"
