@@ -58,11 +58,13 @@ int geometry(int64_t B, int64_t Hq, int64_t Hkv, int64_t D, Geometry& g) {
 // than CUs: smaller items give the split more, shorter pieces to share out,
 // and once there is an item per work-group every output row is written
 // directly, with nothing for the split-K merge.  A contiguous cache takes the
-// halved IU.  A paged pool takes it only when it reaches an item per CU (B64
-// x 8 KV heads: 2 units of 4 waves, config 3 182.5 -> 180.6 us per call):
-// a page holds every KV head's 16 tokens side by side, the waves of a wide
-// item read them together, and narrower items that still leave a split ran
-// config 2's main kernel 2-2.5 us (7%) slower.
+// halved IU.  A paged pool takes it when it reaches an item per CU (B64 x 8
+// KV heads: 2 units of 4 waves, config 3 182.5 -> 180.6 us per call) or holds
+// at most 4 sequences (each otherwise split into up to hundreds of pieces:
+// B1 x 8192 tokens 20.2 -> 16.7 us with inputs rotated past the MALL).
+// Otherwise it keeps wide items: a page holds every KV head's 16 tokens side
+// by side and the waves of a wide item read them together; narrower items
+// that still leave a split ran config 2's main kernel 2-2.5 us (7%) slower.
 void item_units(Geometry& g, bool paged) {
   const int nw = decode_waves(g.D);
   const int cus = device_info().cus > 0 ? device_info().cus : 256;
@@ -70,7 +72,7 @@ void item_units(Geometry& g, bool paged) {
   g.IU = g.U < nw ? g.U : nw;
   int iu = g.IU;
   while (iu % 2 == 0 && items(iu) < cus) iu /= 2;
-  if (!paged || items(iu) >= cus) g.IU = iu;
+  if (!paged || items(iu) >= cus || g.B <= 4) g.IU = iu;
   g.UB = (g.U + g.IU - 1) / g.IU;
 }
 
