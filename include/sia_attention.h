@@ -4,8 +4,10 @@
  * Each entry point replaces one function of the reference engine's attention
  * path (Prathmesh234/simple-inference-autoresearch); the reference interface it
  * stands in for is cited above it as file:line.  The Python package next to
- * this header binds these symbols with ctypes and keeps the reference's Python
- * signatures; any other FFI (cgo, JNI, N-API) can bind them the same way.
+ * this header calls these symbols from its thin PyTorch extension (`_sia_ops`,
+ * C++) and keeps the reference's Python signatures; it also opens the library
+ * with ctypes for the version, status strings and the tests that call the ABI
+ * directly.  Any other FFI (cgo, JNI, N-API) can bind them the same way.
  *
  * Conventions shared by every entry point
  *  - Tensors are passed as `sia_tensor` descriptors: a device pointer, a dtype,

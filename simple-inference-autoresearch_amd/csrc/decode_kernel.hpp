@@ -860,6 +860,9 @@ void decode_main(const DecodeArgs a) {
         const int r2 = idx - us * nh_all * D;
         const int cc = r2 / D, d = r2 - cc * D;
         const int u2 = ublk * shape.units + us;
+        // the last unit block of a geometry whose IU does not divide U has
+        // slots past the last unit: they own no output row
+        if (u2 >= a.U) continue;
         const int hkv2 = u2 / a.HG, hg2 = u2 - hkv2 * a.HG;
         if (16 * hg2 + cc >= a.G) continue;
         float M = -INFINITY;

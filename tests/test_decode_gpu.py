@@ -1,12 +1,11 @@
 """GPU parity of the decode family against the float64 oracle.
 
 Tolerances (stated per the north star):
-* fp16/bf16 K/V: max-abs <= 2e-3 against the oracle, or within one unit in
-  the last place of the output dtype where |ref| is large enough that a single
-  output rounding step exceeds 2e-3 (bf16 ulp at |o| >= 0.25).
+* fp16/bf16 K/V: max-abs <= 2e-3 against the oracle before one rounding to
+  the output dtype: |got - ref| <= 2e-3 + 1/2 ulp(|ref| + 2e-3).
 * int8 K/V: max-abs <= 1e-2 against attention over the dequantised K/V (the
-  reference's own dequantised path); the measured error is far smaller and a
-  tighter 2e-3-or-1-ulp bound is asserted too.
+  reference's own dequantised path), in the same before-rounding form; the
+  measured error is far smaller and the 2e-3 bar is asserted too.
 Full BASELINE sizes are covered by an oracle check of a subset of sequences
 plus size-independent properties (split-count invariance, page-permutation
 invariance, identity-table == contiguous).
@@ -20,34 +19,11 @@ import pytest
 import torch
 
 from oracle import attention as O
-from helpers import announce
+from helpers import announce, assert_close, f64
 
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-
-
-def f64(t: torch.Tensor) -> np.ndarray:
-    return t.detach().float().cpu().numpy().astype(np.float64)
-
-
-def ulp(x: np.ndarray, dtype: torch.dtype) -> np.ndarray:
-    mant = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}[dtype]
-    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -24)))
-    return 2.0 ** (e - mant)
-
-
-def assert_close(got: torch.Tensor, ref: np.ndarray, atol: float, what: str):
-    g = f64(got)
-    assert g.shape == ref.shape, (g.shape, ref.shape)
-    assert np.isfinite(g).all(), f"{what}: non-finite output"
-    err = np.abs(g - ref)
-    allowed = np.maximum(atol, ulp(ref, got.dtype))
-    worst = np.unravel_index(np.argmax(err - allowed), err.shape)
-    assert (err <= allowed).all(), (
-        f"{what}: max err {err.max():.3e} (at {worst}: got {g[worst]:.6f} ref {ref[worst]:.6f}, "
-        f"allowed {allowed[worst]:.2e})")
-    return float(err.max())
 
 
 def contiguous_case(B, Hq, Hkv, S, D, kv_dtype, q_dtype, seed, scale_dtype=torch.float32):

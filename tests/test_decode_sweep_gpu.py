@@ -3,11 +3,13 @@
 Each case draws (head_dim, KV heads, GQA group, batch, cache length, layout,
 K/V dtype, scale dtype, page size, per-sequence lengths) from a fixed
 generator, so a failure names a case that reruns identically.  The shapes
-cover how a call's work is cut: odd unit counts (3, 5, 6 KV heads), groups of
-more than 16 query heads (two head groups per KV head), single sequences and
-batches above and below the CU count, contiguous caches and paged pools.
-Tolerance as in the other decode tests: 2e-3 (or one output ulp) for 16-bit
-K/V, and for int8 against attention over the dequantised cache.
+cover how a call's work is cut: odd unit counts (3, 5, 6, 7, 9, 10 KV heads),
+groups of more than 16 query heads (two head groups per KV head), single
+sequences and batches above and below the CU count (52-127 sequences make
+the host halve the units per work-group item to a count that need not divide
+the unit count), contiguous caches and paged pools.  Tolerance as in the
+other decode tests: 2e-3 before one output rounding, for 16-bit K/V against
+the oracle and for int8 against attention over the dequantised cache.
 """
 
 from __future__ import annotations
@@ -18,28 +20,20 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import announce
+from helpers import announce, assert_close, f64
 from oracle import attention as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-N_CASES = 32
-
-
-def f64(t):
-    return t.detach().float().cpu().numpy().astype(np.float64)
-
-
-def ulp(x, dtype):
-    mant = {torch.bfloat16: 7, torch.float16: 10}[dtype]
-    return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -24))) - mant)
+N_CASES = 40
 
 
 def draw(i: int) -> dict:
     r = random.Random(1000 + i)
     while True:
-        c = dict(D=r.choice([64, 128, 256]), Hkv=r.choice([1, 2, 3, 4, 5, 6, 8]),
-                 G=r.choice([1, 2, 3, 4, 5, 8, 12, 16, 20, 32]), B=r.choice([1, 2, 3, 5, 16, 40, 64, 130]),
+        c = dict(D=r.choice([64, 128, 256]), Hkv=r.choice([1, 2, 3, 4, 5, 6, 7, 8, 9, 10]),
+                 G=r.choice([1, 2, 3, 4, 5, 8, 12, 16, 20, 32]),
+                 B=r.choice([1, 2, 3, 5, 16, 40, 52, 64, 86, 100, 127, 130]),
                  S=r.choice([16, 100, 700, 2048]), paged=r.random() < 0.5, kv=r.choice(["bf16", "fp16", "int8"]),
                  sd=r.choice([torch.float32, torch.float16]), page=r.choice([16, 32]))
         if c["B"] * c["Hkv"] * c["G"] * c["S"] * c["D"] <= 24_000_000:
@@ -92,8 +86,4 @@ def test_random_decode_shape(gpu_pkg, i):
             out = gpu_pkg.attention_flash_decode(q, k, v, kl)
             ref = O.gqa_decode(f64(q), f64(k), f64(v), c["lens"])
     torch.cuda.synchronize()
-    got = f64(out)
-    assert got.shape == ref.shape and np.isfinite(got).all()
-    err = np.abs(got - ref)
-    allowed = np.maximum(2e-3, ulp(ref, out.dtype))
-    assert (err <= allowed).all(), f"case {i} {c}: max err {err.max():.3e}"
+    assert_close(out, ref, 2e-3, f"case {i} {c}")

@@ -6,7 +6,7 @@ its decode kernel computes in fp32 on vector lanes.  Float32 q or K/V run on
 this library's fp32 vector-ALU kernel, so the bar is fp32 rounding: max-abs
 <= 1e-5 against the float64 oracle for N(0,1) inputs (outputs are O(1)).
 Calls that mix a 16-bit q with fp32 K/V return q's dtype and are held to the
-16-bit bar (2e-3 or one output ulp).
+16-bit bar (2e-3 before one output rounding).
 """
 
 from __future__ import annotations

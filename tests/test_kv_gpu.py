@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import announce
+from helpers import announce, assert_close, f64
 from oracle import attention as O
 
 pytestmark = pytest.mark.gpu
@@ -23,21 +23,8 @@ DEV = "cuda"
 _NP_DT = {torch.bfloat16: "bfloat16", torch.float16: "float16", torch.float32: "float32"}
 
 
-def f64(t):
-    return t.detach().float().cpu().numpy().astype(np.float64)
-
-
-def ulp(x, dtype):
-    mant = {torch.bfloat16: 7, torch.float16: 10, torch.float32: 23}[dtype]
-    return 2.0 ** (np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** -24))) - mant)
-
-
 def close(got, ref, what, atol):
-    g = f64(got)
-    assert np.isfinite(g).all(), what
-    err = np.abs(g - ref)
-    allowed = np.maximum(atol, ulp(ref, got.dtype))
-    assert (err <= allowed).all(), f"{what}: max err {err.max():.3e}"
+    assert_close(got, ref, atol, what)
 
 
 def oracle_quant(x: torch.Tensor, scale_dtype: torch.dtype):

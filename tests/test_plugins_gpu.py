@@ -1,6 +1,6 @@
 """GPU checks of the plugin boundary: llama cache builder and the Qwen3.5 attention interface.
 
-* ``sia_attention_forward`` against the float64 oracle (2e-3 or one output ulp).
+* ``sia_attention_forward`` against the float64 oracle (2e-3 before one output rounding).
 * A small randomly initialised Qwen3.5 text model whose layers are all full
   attention (head_dim 256, 8 query / 2 KV heads): run on the GPU in bf16
   through the registered kernels, and as the reference on the CPU in fp32 with
@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import announce
+from helpers import announce, assert_close
 from oracle import attention as O
 
 pytestmark = pytest.mark.gpu
@@ -48,9 +48,7 @@ def test_attention_function_matches_oracle(gpu_pkg, T, S, D):
     torch.cuda.synchronize()
     assert w is None and out.shape == (2, T, 8, D)
     ref = O.flash_attention(f64(q), f64(k), f64(v), True, D ** -0.5)     # (B, Hq, T, D)
-    got = f64(out.transpose(1, 2))
-    ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -24))) - 7)
-    assert (np.abs(got - ref) <= np.maximum(2e-3, ulp)).all(), np.abs(got - ref).max()
+    assert_close(out.transpose(1, 2), ref, 2e-3, f"T={T} S={S} D={D}")
 
 
 def test_attention_function_rejects_padding(gpu_pkg):
@@ -70,7 +68,7 @@ def test_attention_function_rejects_padding(gpu_pkg):
 def test_attention_function_decode_step_in_hip_graph(gpu_pkg):
     """A Qwen3.5 decode step (Tq = 1, head_dim 256, 8/2 heads) through sia_attention_forward,
     captured once in a HIP graph and replayed with new query and cache contents: every
-    replay equals the eager call bit for bit and the oracle within 2e-3 or one ulp."""
+    replay equals the eager call bit for bit and the oracle within 2e-3 before one rounding."""
     announce("sia_attention_forward decode step under HIP-graph capture")
     B, Hq, Hkv, S, D = 2, 8, 2, 300, 256
     g = torch.Generator(device=DEV).manual_seed(77)
@@ -95,9 +93,7 @@ def test_attention_function_decode_step_in_hip_graph(gpu_pkg):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i} differs from the eager call"
         ref = O.flash_attention(f64(q), f64(k), f64(v), True, D ** -0.5)
-        got = f64(out.transpose(1, 2))
-        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -24))) - 7)
-        assert (np.abs(got - ref) <= np.maximum(2e-3, ulp)).all(), np.abs(got - ref).max()
+        assert_close(out.transpose(1, 2), ref, 2e-3, f"replay {i}")
 
 
 def test_qwen35_full_attention_model(gpu_pkg):
