@@ -117,7 +117,9 @@ int sia_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_int8,
 
 /* Replaces paged_attention_flash_decode (kernels/paged_flash_decode_kernel.py:107-152).
  * k_pool,v_pool (num_pages,Hkv,page_size,D) f16|bf16; block_table (B,max_blocks)
- * int32; page_size a multiple of 16 (16 * 2^k). */
+ * int32; page_size any positive size: 16 * 2^k runs on the MFMA kernels, any
+ * other size (1, 2, 4, 8, ... as the reference's tl.arange(0, PAGE_SIZE)
+ * takes) on the fp32 vector-ALU kernel, which looks up each token's page. */
 int sia_paged_attention_flash_decode(const sia_tensor* q, const sia_tensor* k_pool,
                                      const sia_tensor* v_pool, const sia_tensor* block_table,
                                      const sia_tensor* kv_len, int32_t page_size, float sm_scale,
@@ -130,7 +132,8 @@ int sia_paged_attention_flash_decode(const sia_tensor* q, const sia_tensor* k_po
  * (kernels/paged_flash_decode_kernel.py:107) and gqa_int8_flash_decode
  * (kernels/paged_flash_decode_int8_gqa_kernel.py:100).
  * k_pool,v_pool (num_pages,Hkv,page_size,D) int8; k_scale_pool,v_scale_pool
- * (num_pages,Hkv,page_size) f32|f16. */
+ * (num_pages,Hkv,page_size) f32|f16; page sizes as for
+ * sia_paged_attention_flash_decode. */
 int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_pool,
                                     const sia_tensor* v_pool, const sia_tensor* k_scale_pool,
                                     const sia_tensor* v_scale_pool,
@@ -148,8 +151,11 @@ int sia_paged_gqa_int8_flash_decode(const sia_tensor* q, const sia_tensor* k_poo
  * geometry whose partials for one work-group per CU do not fit that array
  * fails with SIA_ERR_WORKSPACE (no valid head_dim/GQA shape does at 64 MiB).
  * Every call on a GPU shares that GPU's array, so calls that overlap on one
- * GPU (concurrent streams, threads) race: serialise them.  Arguments,
- * results and errors are otherwise those of sia_paged_gqa_int8_flash_decode. */
+ * GPU (concurrent streams, threads) race: serialise them.  The array is
+ * part of the library's code object, so every GPU on which any kernel of the
+ * library is loaded holds its 64 MiB, whether or not this entry point is
+ * called.  Arguments, results and errors are otherwise those of
+ * sia_paged_gqa_int8_flash_decode. */
 #define SIA_NOALLOC_SCRATCH_BYTES (64u << 20)
 int sia_paged_gqa_int8_flash_decode_noalloc(const sia_tensor* q, const sia_tensor* k_pool,
                                             const sia_tensor* v_pool, const sia_tensor* k_scale_pool,

@@ -339,6 +339,19 @@ int launch_attn_f32(F32Launch& L) {
   } else if (L.kv_dtype == SIA_F32) {
     if (L.q_dtype == SIA_F16) return launch_f32_d<F16, F32, F32>(L);
     if (L.q_dtype == SIA_BF16) return launch_f32_d<BF16, F32, F32>(L);
+  } else {
+    // 16-bit q over a paged pool whose pages are not whole 16-token tiles
+    // (page sizes 1-8 and the like): 16-bit or int8 K/V
+    const bool h = L.q_dtype == SIA_F16;
+    if (L.q_dtype != SIA_F16 && L.q_dtype != SIA_BF16) return fail(SIA_ERR_UNSUPPORTED, "q dtype not supported");
+    switch (L.kv_dtype) {
+      case SIA_F16: return h ? launch_f32_d<F16, F16, F32>(L) : launch_f32_d<BF16, F16, F32>(L);
+      case SIA_BF16: return h ? launch_f32_d<F16, BF16, F32>(L) : launch_f32_d<BF16, BF16, F32>(L);
+      case SIA_I8:
+        if (L.scale_dtype == SIA_F16) return h ? launch_f32_d<F16, I8, F16>(L) : launch_f32_d<BF16, I8, F16>(L);
+        return h ? launch_f32_d<F16, I8, F32>(L) : launch_f32_d<BF16, I8, F32>(L);
+      default: break;
+    }
   }
   return fail(SIA_ERR_UNSUPPORTED, "fp32 attention: q %s with K/V %s not supported", dtype_name(L.q_dtype),
               dtype_name(L.kv_dtype));

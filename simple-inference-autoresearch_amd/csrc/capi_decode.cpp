@@ -160,12 +160,14 @@ int prepare_kv(const sia_tensor* k, const sia_tensor* v, const Geometry& g, bool
   if (paged) {
     if (k->shape[2] != page_size)
       return fail(SIA_ERR_INVALID_ARGUMENT, "k_pool page dim %lld != page_size %d", (long long)k->shape[2], page_size);
-    if (page_size < 16 || page_size % 16 || ((page_size / 16) & (page_size / 16 - 1)))
-      return fail(SIA_ERR_UNSUPPORTED, "page_size %d: this build supports 16 * 2^k", page_size);
+    if (page_size < 1) return fail(SIA_ERR_INVALID_ARGUMENT, "page_size %d must be positive", page_size);
+    // 16 * 2^k: whole 16-token tiles per page (the MFMA kernels); any other
+    // page size runs on the vector-ALU path, which looks up every token's page
     int lg = 0;
     while ((16 << lg) < page_size) ++lg;
-    a.lg_tiles_per_page = lg;
+    a.lg_tiles_per_page = (16 << lg) == page_size ? lg : 0;
     a.num_pages = k->shape[0];
+    L.page_size = page_size;
   } else {
     if (k->shape[0] < g.B) return fail(SIA_ERR_INVALID_ARGUMENT, "k/v batch dim smaller than q's");
     if (k->shape[2] > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "cache length too large");
@@ -246,9 +248,10 @@ int prepare_workspace(void* ws, size_t bytes, const Geometry& g, const sia_decod
   return SIA_OK;
 }
 
-// Float32 q or K/V: the vector-ALU path (attn_f32.hpp).  Same checked
-// arguments as the MFMA path; the key range is split on the host from the
-// cache capacity so that the partials fit the caller's workspace.
+// Float32 q or K/V, or pages of a size other than 16 * 2^k: the vector-ALU
+// path (attn_f32.hpp), which finds each token's page on its own.  Same
+// checked arguments as the MFMA path; the key range is split on the host
+// from the cache capacity so that the partials fit the caller's workspace.
 int dispatch_f32(const DecodeLaunch& D, const Geometry& g, int kv_dtype, const sia_tensor* out) {
   const DecodeArgs& d = D.a;
   if (!aligned16(out->data) || bstride(out, 0) % 16 || bstride(out, 2) % 16)
@@ -264,7 +267,7 @@ int dispatch_f32(const DecodeLaunch& D, const Geometry& g, int kv_dtype, const s
   a.vs = d.vs; a.vs_s0 = d.vs_s0; a.vs_sh = d.vs_sh; a.vs_sn = d.vs_sn;
   a.bt = d.bt; a.bt_sb = d.bt_sb; a.bt_sl = d.bt_sl;
   a.num_pages = d.num_pages;
-  a.page_size = kTile << d.lg_tiles_per_page;
+  a.page_size = D.page_size > 0 ? D.page_size : 1;
   a.kv_len = d.kv_len; a.kv_per_seq = d.kv_per_seq;
   a.cap = d.cap_tokens;
   a.B = g.B; a.Hq = g.Hq; a.Hkv = g.Hkv; a.G = g.G; a.Tq = 1; a.Tk = d.cap_tokens; a.causal = 0;
@@ -350,7 +353,10 @@ int decode_any(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, co
   L.stream = (hipStream_t)stream;
   L.ws = ws;
   L.ws_bytes = ws_bytes;
-  if (q->dtype == SIA_F32 || k->dtype == SIA_F32) return dispatch_f32(L, g, k->dtype, out);
+  // pages that do not hold whole 16-token tiles (page sizes 1-8, or any size
+  // other than 16 * 2^k) go to the vector-ALU path with its per-token lookup
+  const bool tiled_pages = bt == nullptr || (kTile << L.a.lg_tiles_per_page) == page_size;
+  if (q->dtype == SIA_F32 || k->dtype == SIA_F32 || !tiled_pages) return dispatch_f32(L, g, k->dtype, out);
   return dispatch(L, k->dtype);
 }
 

@@ -27,6 +27,7 @@ struct DecodeLaunch {
   hipEvent_t end_event;
   void* ws;                 // the caller's workspace (the fp32 path lays it out itself)
   size_t ws_bytes;
+  int page_size;            // paged pools: tokens per page (0: contiguous cache)
 };
 
 inline size_t decode_lds_bytes(int D, int G16, int B, int NW) {

@@ -582,21 +582,27 @@ void prefill_fwd(const PrefillArgs a) {
     }
   };
   // row max over the 64 keys: a lane-local tree plus the partner half of the wave
+  // (a three-input tree, 32 values in 16 v_maximum3; pairs of two-input
+  // maxima had compiled to 21, several of them with a repeated operand)
   auto rowmax = [&](const f32x16& s0, const f32x16& s1) {
-    float mx[8];
+    auto mx3 = [](float x, float y, float z) {
+      return __builtin_elementwise_maximum(__builtin_elementwise_maximum(x, y), z);
+    };
+    float v[32];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      mx[j] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s0[4 * j], s0[4 * j + 1]),
-                                            __builtin_elementwise_maximum(s0[4 * j + 2], s0[4 * j + 3]));
-      mx[4 + j] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(s1[4 * j], s1[4 * j + 1]),
-                                                __builtin_elementwise_maximum(s1[4 * j + 2], s1[4 * j + 3]));
+    for (int j = 0; j < 16; ++j) {
+      v[j] = s0[j];
+      v[16 + j] = s1[j];
     }
-    const float r = __builtin_elementwise_maximum(
-        __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx[0], mx[1]),
-                                      __builtin_elementwise_maximum(mx[2], mx[3])),
-        __builtin_elementwise_maximum(__builtin_elementwise_maximum(mx[4], mx[5]),
-                                      __builtin_elementwise_maximum(mx[6], mx[7])));
-    return half_swap_max(r);
+    float t[12];
+#pragma unroll
+    for (int i = 0; i < 10; ++i) t[i] = mx3(v[3 * i], v[3 * i + 1], v[3 * i + 2]);
+    t[10] = v[30];
+    t[11] = v[31];
+    float u[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) u[i] = mx3(t[3 * i], t[3 * i + 1], t[3 * i + 2]);
+    return half_swap_max(__builtin_elementwise_maximum(mx3(u[0], u[1], u[2]), u[3]));
   };
   // lazy running max: (l, o) are rescaled only when the block max exceeds m by
   // 2^8 (p <= 2^8 otherwise, well inside f16)
@@ -699,7 +705,7 @@ void prefill_fwd(const PrefillArgs a) {
       // instructions counted apart.  24 exponentials of P_j (k-slots 0-2)
       // and their 48 fma/pack/row-sum instructions go under the QK slots, 8
       // (k-slot 3) and 16 under the first half of the PV slots, the row max
-      // (~23 instructions) under the rest.
+      // (~19 instructions with the swap and the rescale test) under the rest.
       constexpr int TQ = (24 + NQK - 1) / NQK, VQ = (48 + NQK - 1) / NQK;
       constexpr int TP = (8 + 2 * ET - 1) / (2 * ET), VP1 = (16 + 2 * ET - 1) / (2 * ET);
       constexpr int VP2 = (24 + 2 * ET - 1) / (2 * ET);

@@ -206,6 +206,25 @@ def test_paged_small(gpu_pkg, kv, page):
     assert_close(out, ref, 2e-3, f"paged {kv} page {page}")
 
 
+@pytest.mark.parametrize("kv", ["fp16", "bf16", "int8"])
+@pytest.mark.parametrize("page", [1, 2, 4, 8, 48])
+def test_paged_pages_below_a_tile(gpu_pkg, kv, page):
+    """Page sizes that do not hold whole 16-token tiles (the reference's
+    tl.arange(0, PAGE_SIZE) takes any power of two, kernels/paged_flash_decode_kernel.py:67):
+    the vector-ALU path looks up every token's page.  Ragged lengths with an
+    empty sequence, 32/8 heads and head_dim 128, and 64/8 at head_dim 64."""
+    announce(f"paged {kv} page={page}")
+    q_dtype = torch.float16 if kv == "fp16" else torch.bfloat16
+    for lens, Hq, D in (([700, 1, 0, 257, 33], 32, 128), ([300, 129], 64, 64)):
+        case = _syn().paged_case(lens, Hq=Hq, Hkv=8, D=D, page=page, seed=13 + page, device=DEV, kv=kv,
+                                 q_dtype=q_dtype, scale_dtype=torch.float16 if page == 4 else torch.float32)
+        out = run_paged(gpu_pkg, case)
+        torch.cuda.synchronize()
+        assert_close(out, oracle_paged(case), 2e-3, f"paged {kv} page {page} D={D}")
+        if 0 in lens:
+            assert torch.all(out[lens.index(0)] == 0)
+
+
 @pytest.mark.parametrize("kv", ["fp16", "int8"])
 @pytest.mark.parametrize("D", [16, 32])
 def test_paged_small_head_dims(gpu_pkg, kv, D):

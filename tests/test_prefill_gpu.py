@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import announce, assert_close, f64
+from helpers import allowed_error, announce, assert_close, f64
 from oracle import attention as O
 
 pytestmark = pytest.mark.gpu
@@ -156,6 +156,37 @@ def test_d128_grid_sizes(gpu_pkg, B, Tq, Tk, causal):
     out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
     torch.cuda.synchronize()
     check_every_head(out, q, k, v, causal, f"B={B} Tq={Tq} Tk={Tk}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_bf16_v_beyond_f16_range_saturates(gpu_pkg, D):
+    """The PV product runs in f16, so bf16 V values beyond the f16 range are
+    saturated to +-65504 (the reference keeps bf16's range,
+    kernels/attention_kernel.py:221).  Pinned: the output matches the oracle
+    over V clamped to +-65504, to 2e-3 plus the f16 rounding of P (2^-11 of
+    sum_k w_k |v_k|, with margin) plus one bf16 output rounding, and it is
+    measurably different from the unclamped oracle on rows that see a
+    saturated key."""
+    announce(f"prefill bf16 V beyond the f16 range D={D}")
+    q, k, v = qkv(1, 4, 2, 96, 96, D, torch.bfloat16, seed=D)
+    v[0, 0, 5, :] = 1.0e5
+    v[0, 1, 9, 3] = -3.0e5
+    v[0, 0, 70, 7] = 7.0e4
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    qf, kf, vf = f64(q), f64(k), f64(v)
+    vc = np.clip(vf, -65504.0, 65504.0)
+    ref = O.flash_attention(qf, kf, vc, True)
+    mag = O.flash_attention(qf, kf, np.abs(vc), True)            # sum_k w_k |v_k|
+    got = f64(out)
+    allowed = allowed_error(ref, torch.bfloat16, 2e-3) + 2.0 ** -10 * mag
+    err = np.abs(got - ref)
+    assert np.isfinite(got).all()
+    assert (err <= allowed).all(), f"max err {err.max():.3e} (allowed there {allowed.flat[np.argmax(err - allowed)]:.3e})"
+    unclamped = O.flash_attention(qf, kf, vf, True)
+    hit = np.abs(unclamped - ref) > 1.0                           # rows/dims a saturated key moves by > 1
+    assert hit.any()
+    assert (np.abs(got - unclamped)[hit] > 0.5).all()
 
 
 def test_prefill_errors(gpu_pkg):
