@@ -628,7 +628,11 @@ void decode_main(const DecodeArgs a) {
   const int W = plan_work<NW>(a, pre, red, tok0, pen);
   int G = (int)gridDim.x;
   if (a.tps_force > 0) G = min(G, max(1, (W + a.tps_force - 1) / a.tps_force));   // forced share (tests)
-  G = min(G, max(1, (W + kMinWaveTiles * shape.P - 1) / (kMinWaveTiles * shape.P)));
+  // least work per group, but never fewer groups than (sequence, unit block)
+  // segments: those are independent, and a group walking several short ones
+  // pays each one's chain of dependent loads in turn (B1 x 16 tokens: 8
+  // segments on one group took ~50 us)
+  G = min(G, max(a.B * a.UB, (W + kMinWaveTiles * shape.P - 1) / (kMinWaveTiles * shape.P)));
   G = min(G, max(1, a.max_items / 2));                      // two partial slots per group
   if (blockIdx.x == 0) {
     for (int i = threadIdx.x; i <= a.B; i += NW * 64) a.ws_plan[kPlanHeader + i] = pre[i];
