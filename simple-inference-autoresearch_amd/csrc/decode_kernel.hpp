@@ -665,26 +665,43 @@ void decode_main(const DecodeArgs a) {
   // block).  A segment that covers its whole (b, ublk) is written straight to
   // `out`; a piece writes a partial to slot 2g (the group's first segment) or
   // 2g+1 (its last), which decode_reduce finds from the same split.
+  //
+  // The segment starting at xs: b is the largest index with pre[b] <= xs.
+  // (A batch-wide length was read once already; per-sequence ones were kept
+  // in LDS by the plan for batches up to kLensInLds, else are read again.)
+  // The line holds each segment as pen virtual tiles (the cost of starting
+  // it: a few dependent memory round trips) followed by its ntile tiles; a
+  // piece of the virtual span maps to real tiles [t_lo, t_hi).
+  struct SegAt {
+    int b, ntok, ntile, ublk, t_lo, t_hi, seg_end;
+  };
+  auto seg_at = [&](int xs) {
+    SegAt s;
+    int blo = 0, bhi = a.B;
+    while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= xs) blo = mid; else bhi = mid; }
+    s.b = uniform(blo);
+    s.ntok = a.kv_per_seq ? uniform(a.B <= kLensInLds ? pre[a.B + 1 + s.b] : seq_tokens(a, s.b)) : tok0;
+    s.ntile = (s.ntok + kTile - 1) / kTile;
+    const int nvt = s.ntile + pen;
+    const int rem = uniform(xs - pre[s.b]);
+    s.ublk = rem / nvt;
+    const int r_lo = rem - s.ublk * nvt;
+    s.seg_end = min(x_hi, pre[s.b] + (s.ublk + 1) * nvt);
+    const int r_hi = r_lo + (s.seg_end - xs);
+    s.t_lo = max(0, r_lo - pen);
+    s.t_hi = max(0, r_hi - pen);
+    return s;
+  };
+  // The next segment's query row and first page id are loaded while the
+  // current one streams (seg_next: the start of the segment they belong
+  // to), so that a segment change waits for its first tile only.
+  QRaw<D> q_next;
+  int pg_next = 0, seg_next = -1;
   bool first_seg = true;
   while (x < x_hi) {
-    // b: the largest index with pre[b] <= x
-    int blo = 0, bhi = a.B;
-    while (bhi - blo > 1) { const int mid = (blo + bhi) >> 1; if (pre[mid] <= x) blo = mid; else bhi = mid; }
-    const int b = uniform(blo);
-    // (a batch-wide length was read once already; per-sequence ones were kept
-    // in LDS by the plan for batches up to kLensInLds, else are read again)
-    const int ntok = a.kv_per_seq ? uniform(a.B <= kLensInLds ? pre[a.B + 1 + b] : seq_tokens(a, b)) : tok0;
-    const int ntile = (ntok + kTile - 1) / kTile;
-    // the line holds each segment as pen virtual tiles (the cost of
-    // starting it: a few dependent memory round trips) followed by its ntile
-    // tiles; a piece of the virtual span maps to real tiles [t_lo, t_hi)
-    const int nvt = ntile + pen;
-    const int rem = uniform(x - pre[b]);
-    const int ublk = rem / nvt;
-    const int r_lo = rem - ublk * nvt;
-    const int seg_end = min(x_hi, pre[b] + (ublk + 1) * nvt);
-    const int r_hi = r_lo + (seg_end - x);
-    const int t_lo = max(0, r_lo - pen), t_hi = max(0, r_hi - pen);
+    const SegAt sg = seg_at(x);
+    const int b = sg.b, ntok = sg.ntok, ntile = sg.ntile, ublk = sg.ublk, t_lo = sg.t_lo, t_hi = sg.t_hi;
+    const int seg_end = sg.seg_end;
     if (t_hi == t_lo) {        // only the start cost of a segment, at the end of the share
       x = seg_end;
       continue;
@@ -719,9 +736,33 @@ void decode_main(const DecodeArgs a) {
         return uniform(btrow[(int64_t)(t >> a.lg_tiles_per_page) * bt_step]);
       };
       // The loads that need only the item go out together: the query row
-      // and the first tile's page id (the length is already in flight).
-      const QRaw<D> qraw = load_q_raw<D, KV>(a, b, hq, live, grp);
-      const int pg0 = page_id(0);
+      // and the first tile's page id (the length is already in flight),
+      // unless the previous segment loaded them already.
+      QRaw<D> qraw;
+      int pg0;
+      if (x == seg_next) {
+        qraw = q_next;
+        pg0 = pg_next;
+      } else {
+        qraw = load_q_raw<D, KV>(a, b, hq, live, grp);
+        pg0 = page_id(0);
+      }
+      // the next segment of the share, if this wave has a unit there: its
+      // query row and first page id (issued behind this segment's first tile)
+      auto prefetch_next = [&]() {
+        if (seg_end >= x_hi) return;
+        const SegAt nx = seg_at(seg_end);
+        const int unit_n = nx.ublk * shape.units + uin;
+        if (nx.t_hi == nx.t_lo || unit_n >= a.U) return;
+        const int hkv_n = unit_n / a.HG, hg_n = unit_n - hkv_n * a.HG;
+        const bool live_n = lane16 < min(16, a.G - 16 * hg_n);
+        const int hq_n = live_n ? hkv_n * a.G + 16 * hg_n + lane16 : 0;
+        q_next = load_q_raw<D, KV>(a, nx.b, hq_n, live_n, grp);
+        const int32_t* btrow_n = paged ? a.bt + (int64_t)nx.b * a.bt_sb : a.kv_len;
+        const int tn = min(nx.t_lo + phase, cap_tiles - 1);
+        pg_next = uniform(btrow_n[(int64_t)(tn >> a.lg_tiles_per_page) * bt_step]);
+        seg_next = seg_end;
+      };
       const int t_full = min(t_hi, ntok / kTile);
       const int nfull = t_first < t_full ? (t_full - t_first + P - 1) / P : 0;
       const int nt = t_first < t_hi ? (t_hi - t_first + P - 1) / P : 0;
@@ -754,11 +795,12 @@ void decode_main(const DecodeArgs a) {
       float qmul = 0.f;
       // Full tiles, double-buffered.  The steady-state loop always issues the
       // next tiles' loads, and fetches the page ids of the tiles two ahead
-      // with one vector load (lanes 0 and 1; indices clamped to the last full
-      // tile), so every load retires in order and computing tile k waits only
-      // for tile k.
+      // with one vector load (lanes 0 and 1; indices clamped to the wave's
+      // last tile, the partial one included), so every load retires in order
+      // and computing tile k waits only for tile k.
+      int pg_last = pg0;   // page of the wave's partial last tile (tile nfull)
       if (nfull > 0) {
-        const int klast = nfull - 1;
+        const int klast = nt > nfull ? nfull : nfull - 1;
         auto page_pair = [&](int k0) {
           const int k = min(k0 + (lane & 1), klast);
           const int t = t_first + k * P;
@@ -769,6 +811,7 @@ void decode_main(const DecodeArgs a) {
         // wait counts where the two paths meet stay exact
         int pgv = page_pair(1);   // tiles k + 1, k + 2
         load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first, pg0), lo, 16, bufA, lane16, grp);
+        prefetch_next();
         // the query's conversion overlaps the first tile's flight
         qmul = prep_q<D, KV, QT>(a, qraw, qop, qop_lo);
         int k = 0;
@@ -795,6 +838,9 @@ void decode_main(const DecodeArgs a) {
           __builtin_amdgcn_s_setprio(0);
           __hip_atomic_store(&prog[wave], 1 << 30, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
+        // pgv holds the pages of tiles k + 1 and k + 2 (clamped); the partial
+        // tile, if any, is tile nfull = k + 1 or k + 2
+        pg_last = __builtin_amdgcn_readlane(pgv, nfull - k - 1);
         if (k + 1 < nfull) {
           load_tile<D, KV, ST, true, SV>(a, tile_ptr(t_first + (k + 1) * P, __builtin_amdgcn_readlane(pgv, 0)), lo,
                                          16, bufB, lane16, grp);
@@ -803,12 +849,14 @@ void decode_main(const DecodeArgs a) {
         } else {
           compute_tile<D, KV, QT, ST, true>(bufA, qop, qop_lo, qmul, 0, ntok, grp, st);
         }
+      } else {
+        prefetch_next();
+        qmul = prep_q<D, KV, QT>(a, qraw, qop, qop_lo);
       }
-      if (nfull == 0) qmul = prep_q<D, KV, QT>(a, qraw, qop, qop_lo);
       if (nt > nfull) {  // the sequence's partial last tile belongs to this wave
         const int t = t_first + nfull * P;
         TileT last;
-        load_tile<D, KV, ST, false, false>(a, tile_ptr(t, page_id(nfull)), lo, ntok - t * kTile, last, lane16, grp);
+        load_tile<D, KV, ST, false, false>(a, tile_ptr(t, pg_last), lo, ntok - t * kTile, last, lane16, grp);
         compute_tile<D, KV, QT, ST, false>(last, qop, qop_lo, qmul, t, ntok, grp, st);
       }
     }
