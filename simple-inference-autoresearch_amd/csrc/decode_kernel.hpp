@@ -73,6 +73,7 @@ struct DecodeArgs {
   int32_t seg_pen;                                   // virtual tiles charged to each segment start (the split)
   int32_t slots;                                     // persistent work-groups of decode_main
   int32_t scale_vec;                                 // scale rows allow one vector load per lane
+  int32_t direct_only;                               // no decode_reduce follows: empty calls write zeros here
   // 32-bit copies of the per-tile strides (bytes): page strides (0 when
   // contiguous) and token strides, so the tile address needs only 32x32->64
   // products
@@ -642,6 +643,18 @@ void decode_main(const DecodeArgs a) {
       a.ws_plan[kPlanUB] = a.UB;
       a.ws_plan[kPlanPen] = pen;
     }
+  }
+  if (a.direct_only && W == 0) {
+    // one shared length of zero, and no merge kernel follows: every output
+    // row is zero (the l == 0 guard), written here as 4-byte words
+    const int64_t words = (int64_t)a.B * a.Hq * (D / 2);
+    for (int64_t i = (int64_t)blockIdx.x * (NW * 64) + threadIdx.x; i < words; i += (int64_t)gridDim.x * (NW * 64)) {
+      const int64_t row = i / (D / 2);
+      const int wd = (int)(i - row * (D / 2));
+      const int bb = (int)(row / a.Hq), hh = (int)(row - (int64_t)bb * a.Hq);
+      *(uint32_t*)(a.out + bb * a.o_sb + (int64_t)hh * a.o_sh + 4 * wd) = 0u;
+    }
+    return;
   }
   const int g = blockIdx.x;
   const int x_hi = g < G ? sk_lo(g + 1, W, G) : 0;

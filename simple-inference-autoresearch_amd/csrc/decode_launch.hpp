@@ -54,7 +54,15 @@ int launch_decode_typed(DecodeLaunch& L) {
   const int occ = kernel_occupancy((const void*)kmain, NW * 64, lds);
   if (occ <= 0) return fail(SIA_ERR_LAUNCH, "decode kernel does not fit on a CU (LDS %zu B)", lds);
   L.a.slots = device_info().cus * occ;
-  // 1. main (persistent, stream-K share per group), 2. merge of the split pieces
+  // One length for the whole batch and a segment count ((sequence, unit
+  // block) pairs) that is a multiple of the persistent grid: the split gives
+  // every group whole segments, so decode_main writes every row itself
+  // (zeros for a zero length) and decode_reduce is not launched.
+  const int64_t nseg = (int64_t)L.a.B * L.a.UB;
+  L.a.direct_only = !L.a.kv_per_seq && L.a.tps_force == 0 && nseg >= L.a.slots && nseg % L.a.slots == 0 &&
+                    L.a.max_items / 2 >= L.a.slots;
+  // 1. main (persistent, stream-K share per group), 2. merge of the split
+  // pieces (unless direct_only)
   if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
   hipLaunchKernelGGL(kmain, dim3(L.a.slots), dim3(NW * 64), lds, L.stream, L.a);
@@ -62,6 +70,7 @@ int launch_decode_typed(DecodeLaunch& L) {
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode launch: %s", hipGetErrorString(e));
   if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
     return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
+  if (L.a.direct_only) return SIA_OK;
   const int rows = L.a.B * L.a.Hq;
   constexpr int kRowsPerGroup = 64 / (D / 4);
   const int ngroups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;

@@ -11,7 +11,10 @@ own no output row.  Every output row is compared with the float64 oracle
 1e-2), for contiguous caches and paged pools, with short equal lengths (every
 segment written directly) and longer ragged ones (split-K pieces).  A call
 through the C ABI writes into a view of a larger buffer whose rows before and
-after hold a sentinel that must survive.
+after hold a sentinel that must survive.  A last test covers calls with one
+shared length whose segments are a multiple of the persistent grid: those
+run the main kernel alone, which then also writes the zero rows of a zero
+length.
 """
 
 from __future__ import annotations
@@ -115,3 +118,64 @@ def test_capi_output_guard(gpu_pkg, D, Hkv, G, B):
     ref = O.paged_decode(f64(case.q), f64(case.k_pool), f64(case.v_pool), case.block_table.cpu().numpy(),
                          case.ctx, case.page_size)
     assert_close(out, ref, 2e-3, "C ABI paged bf16")
+
+
+@pytest.mark.parametrize("kv", ["bf16", "int8"])
+@pytest.mark.parametrize("paged", [False, True])
+def test_shared_length_whole_segment_split(gpu_pkg, kv, paged):
+    """One shared length (kv_len of one element) over 64 sequences x 8 KV heads:
+    the segments are a multiple of the persistent grid, every group gets whole
+    segments and the call is the main kernel alone (no merge kernel).  Lengths
+    0 (every row zero), 1, 100 and 1000, through the C ABI into a NaN-filled
+    output, against the float64 oracle."""
+    h = L.require_library()
+    B, Hq, Hkv, D = 64, 32, 8, 128
+    for n in (0, 1, 100, 1000):
+        announce(f"shared length {n}: {kv} {'paged' if paged else 'contiguous'} B={B}")
+        if paged:
+            case = syn.paged_case([max(n, 1)] * B, Hq=Hq, Hkv=Hkv, D=D, page=16, seed=7 + n, device=DEV, kv=kv,
+                                  q_dtype=torch.bfloat16, per_seq_len=False)
+            tensors = [case.q, case.k_pool, case.v_pool] + ([case.k_scale, case.v_scale] if kv == "int8" else []) + \
+                      [case.block_table]
+            q = case.q
+        else:
+            g = torch.Generator(device=DEV).manual_seed(n)
+            q = torch.randn(B, Hq, 1, D, generator=g, device=DEV).to(torch.bfloat16)
+            kf = torch.randn(B, Hkv, max(n, 1), D, generator=g, device=DEV)
+            vf = torch.randn(B, Hkv, max(n, 1), D, generator=g, device=DEV)
+            if kv == "int8":
+                ki, ks = syn.quantize_per_vector(kf, torch.float32)
+                vi, vs = syn.quantize_per_vector(vf, torch.float32)
+                tensors = [q, ki, vi, ks, vs]
+            else:
+                tensors = [q, kf.to(torch.bfloat16), vf.to(torch.bfloat16)]
+        kl = torch.full((1,), n, dtype=torch.int32, device=DEV)
+        out = torch.full((B, 1, Hq, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+        ws = torch.empty(gpu_pkg.decode_workspace_size(B, Hq, Hkv, D), dtype=torch.uint8, device=DEV)
+        ds = [L.desc(t) for t in tensors] + [L.desc(kl)]
+        tail = [ctypes.c_float(D ** -0.5), ctypes.byref(L.desc(out)), ctypes.c_void_p(ws.data_ptr()),
+                ctypes.c_size_t(ws.numel()), None, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)]
+        if paged:
+            fn = h.sia_paged_gqa_int8_flash_decode if kv == "int8" else h.sia_paged_attention_flash_decode
+            rc = fn(*[ctypes.byref(d) for d in ds], ctypes.c_int32(16), *tail)
+        else:
+            fn = h.sia_attention_flash_decode_int8 if kv == "int8" else h.sia_attention_flash_decode
+            rc = fn(*[ctypes.byref(d) for d in ds], *tail)
+        assert rc == 0, h.sia_last_error_message()
+        torch.cuda.synchronize()
+        if n == 0:
+            assert bool((out == 0).all()), "a zero length must give zero rows"
+            continue
+        if paged:
+            if kv == "int8":
+                ref = O.paged_int8_decode(f64(q), case.k_pool.cpu().numpy(), case.v_pool.cpu().numpy(),
+                                          f64(case.k_scale), f64(case.v_scale), case.block_table.cpu().numpy(),
+                                          [n] * B, 16)
+            else:
+                ref = O.paged_decode(f64(q), f64(case.k_pool), f64(case.v_pool), case.block_table.cpu().numpy(),
+                                     [n] * B, 16)
+        elif kv == "int8":
+            ref = O.int8_decode(f64(q), ki.cpu().numpy(), vi.cpu().numpy(), f64(ks), f64(vs), [n] * B)
+        else:
+            ref = O.gqa_decode(f64(q), f64(tensors[1]), f64(tensors[2]), [n] * B)
+        assert_close(out, ref, 1e-2 if kv == "int8" else 2e-3, f"shared length {n}")
