@@ -36,12 +36,15 @@ from . import _lib
 _HEAD_DIMS = (16, 32, 64, 128, 256)
 _tls = threading.local()
 _ws_cache: dict = {}
+# decode_options blocks active in any thread (their options are thread-local;
+# with none active a call skips the thread-local lookups)
+_opts_users = 0
+_opts_lock = threading.Lock()
+_OPS = None   # the extension module, once loaded on a GPU
 
-
-def _fail(cond: bool, msg: str) -> None:
-    """The reference wrappers assert; raise the same AssertionError (even under -O)."""
-    if not cond:
-        raise AssertionError(msg)
+# The reference wrappers assert; these raise the same AssertionError (even
+# under -O), testing the condition first so that no message is formatted on
+# a call that passes.
 
 
 @contextlib.contextmanager
@@ -53,13 +56,18 @@ def decode_options(tiles_per_split: int = 0, main_events=None):
         library records them on the launch stream around the main decode
         kernel (excluding the split-K reduction), for kernel timing.
     """
+    global _opts_users
     prev = (getattr(_tls, "tiles_per_split", 0), getattr(_tls, "main_events", None))
     _tls.tiles_per_split = int(tiles_per_split)
     _tls.main_events = main_events
+    with _opts_lock:
+        _opts_users += 1
     try:
         yield
     finally:
         _tls.tiles_per_split, _tls.main_events = prev
+        with _opts_lock:
+            _opts_users -= 1
 
 
 def decode_workspace_size(batch: int, num_q_heads: int, num_kv_heads: int, head_dim: int) -> int:
@@ -87,19 +95,25 @@ CONTIG, CONTIG_INT8, GQA_INT8, PAGED, PAGED_INT8 = range(5)
 def _run(kind: int, q: torch.Tensor, k, v, k_scale, v_scale, block_table, kv_len, page_size: int,
          sm_scale: float) -> torch.Tensor:
     """One decode call through the torch extension (device checks, output and workspace in C++)."""
-    ops = _lib.gpu_ops()
-    tps = getattr(_tls, "tiles_per_split", 0)
-    ev = getattr(_tls, "main_events", None)
-    b = e = 0
-    if ev is not None:
-        b, e = ev[0].cuda_event, ev[1].cuda_event
+    global _OPS
+    ops = _OPS
+    if ops is None:
+        ops = _OPS = _lib.gpu_ops()
+    tps = b = e = 0
+    if _opts_users:
+        tps = getattr(_tls, "tiles_per_split", 0)
+        ev = getattr(_tls, "main_events", None)
+        if ev is not None:
+            b, e = ev[0].cuda_event, ev[1].cuda_event
     return ops.decode(kind, q, k, v, k_scale, v_scale, block_table, kv_len, page_size, sm_scale, tps, b, e)
 
 
 def _common(q: torch.Tensor, k: torch.Tensor, sm_scale):
     B, Hq, Tq, D = q.shape
-    _fail(Tq == 1, "decode kernel expects a single query position")
-    _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
+    if Tq != 1:
+        raise AssertionError("decode kernel expects a single query position")
+    if D not in _HEAD_DIMS:
+        raise AssertionError(f"unsupported head_dim {D}")
     return (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
 
 
@@ -147,11 +161,15 @@ def paged_attention_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: 
     k_pool, v_pool: (num_blocks, Hkv, page_size, D); block_table: (B, max_blocks)
     int32 logical->physical page ids.
     """
-    B, Hq, Tq, D = q.shape
-    _, Hkv, P, _ = k_pool.shape
-    _fail(Tq == 1, "decode kernel expects a single query position")
-    _fail(P == page_size, f"k_pool page dim {P} != page_size {page_size}")
-    _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
+    Tq, D = q.shape[2], q.shape[3]
+    P = k_pool.shape[2]
+    # the reference's asserts, in its order (kernels/paged_flash_decode_kernel.py:131-134)
+    if Tq != 1:
+        raise AssertionError("decode kernel expects a single query position")
+    if P != page_size:
+        raise AssertionError(f"k_pool page dim {P} != page_size {page_size}")
+    if D not in _HEAD_DIMS:
+        raise AssertionError(f"unsupported head_dim {D}")
     scale = (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
     kl = _kv_len_tensor(kv_len, q.device)
     return _run(PAGED, q, k_pool, v_pool, None, None, block_table, kl, page_size, scale)
@@ -167,11 +185,15 @@ def paged_gqa_int8_flash_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: t
     v_scale_pool: (num_blocks, Hkv, page_size) fp32 or fp16; block_table
     (B, max_blocks) int32; kv_len (1,)/() or (B,) int32.
     """
-    B, Hq, Tq, D = q.shape
-    _, Hkv, P, _ = k_pool.shape
-    _fail(Tq == 1, "decode kernel expects a single query position")
-    _fail(P == page_size, f"k_pool page dim {P} != page_size {page_size}")
-    _fail(D in _HEAD_DIMS, f"unsupported head_dim {D}")
+    Tq, D = q.shape[2], q.shape[3]
+    P = k_pool.shape[2]
+    # the reference's asserts, in its order (kernels/paged_flash_decode_kernel.py:131-134)
+    if Tq != 1:
+        raise AssertionError("decode kernel expects a single query position")
+    if P != page_size:
+        raise AssertionError(f"k_pool page dim {P} != page_size {page_size}")
+    if D not in _HEAD_DIMS:
+        raise AssertionError(f"unsupported head_dim {D}")
     scale = (1.0 / (D ** 0.5)) if sm_scale is None else float(sm_scale)
     kl = _kv_len_tensor(kv_len, q.device)
     return _run(PAGED_INT8, q, k_pool, v_pool, k_scale_pool, v_scale_pool, block_table, kl, page_size, scale)
