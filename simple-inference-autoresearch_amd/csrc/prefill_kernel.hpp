@@ -749,6 +749,69 @@ void prefill_fwd(const PrefillArgs a) {
       rmax = rowmax(s0, s1);
     }
   };
+  // The work-group's last key block T = nblk - 1 runs after the loop: its
+  // PV product alone (no next block's scores to compute).  When every row of
+  // the wave sees at most the block's first 32 keys (a causal diagonal block
+  // whose second half lies past the wave's rows, or a ragged last block), the
+  // second key tile's weights are all zero and its exponentials and PV MFMAs
+  // are skipped.  Its V stage is picked at run time (one block per group).
+  const int wlim = a.causal ? min(a.Tk - 1, off + wrow0 + 31) : a.Tk - 1;   // the wave's last visible key
+  auto work_last = [&](const char* Vstage, int j, const f32x16& sa0, const f32x16& sa1) {
+    if (j >= wblk) return;
+    raise_max(rmax);
+    const char* V = Vstage + h * DV * 16 + l32 * 16;
+    const float mu = m == -INFINITY ? 0.f : m;
+    const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+    u32x4 pop[4];
+    float lb[4];
+    auto ex = [&](int ks) {
+      lb[ks] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int j0 = (ks & 1) * 8 + 2 * i;
+        const float x0 = ks < 2 ? sa0[j0] : sa1[j0];
+        const float x1 = ks < 2 ? sa0[j0 + 1] : sa1[j0 + 1];
+        const float p0 = fast_exp2(__builtin_fmaf(x0, a.qk_scale, -mu));
+        const float p1 = fast_exp2(__builtin_fmaf(x1, a.qk_scale, -mu));
+        const uint32_t w = pack2(F16{}, p0, p1);
+        lb[ks] = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, w), ones, lb[ks], false);
+        pop[ks][i] = w;
+      }
+    };
+    auto rdv = [&](int x) { return *(const u32x4*)(V + (x / ET) * 2 * DV * 16 + (x % ET) * 512); };
+    auto pv = [&](auto nks) {
+      constexpr int NX = decltype(nks)::value * ET;
+      u32x4 buf[3];
+      buf[0] = rdv(0);
+      buf[1] = rdv(1);
+#pragma unroll
+      for (int ks = 0; ks < decltype(nks)::value; ++ks) ex(ks);
+#pragma unroll
+      for (int x = 0; x < NX; ++x) {
+        if (x + 2 < NX) buf[(x + 2) % 3] = rdv(x + 2);
+        o[x % ET] = mfma32x32x16(F16{}, buf[x % 3], pop[x / ET], o[x % ET]);
+      }
+    };
+    if (wlim < j * kPfBN + 32) {
+      pv(std::integral_constant<int, 2>{});
+      l += lb[0] + lb[1];
+    } else {
+      pv(std::integral_constant<int, 4>{});
+      l += (lb[0] + lb[1]) + (lb[2] + lb[3]);
+    }
+  };
+  // scores of block nfb (the last): in s after an even number of full blocks, in n after an odd one
+  const int nfb = nblk > 0 ? nblk - 1 : 0;
+  auto last_block = [&](const char* Vstage) {
+    f32x16 t0, t1;
+    const bool in_n = (nfb & 1) != 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      t0[i] = in_n ? n0[i] : s0[i];
+      t1[i] = in_n ? n1[i] : s1[i];
+    }
+    work_last(Vstage, nfb, t0, t1);
+  };
 
   if constexpr (S == 4) {
     // Four-stage ring, one barrier per two key blocks.  Block j needs K_{j+1}
@@ -836,13 +899,20 @@ void prefill_fwd(const PrefillArgs a) {
     } else {
       load_q();
     }
+    // blocks 0 .. nblk - 2 in full steps, then the last block's PV product
     int j = 0;
-    for (; j + 3 < nblk; j += 4) {
+    for (; j + 3 < nfb; j += 4) {
       super(PfParity<0>{}, j, true);
       super(PfParity<2>{}, j + 2, true);
     }
-    if (j < nblk) super(PfParity<0>{}, j, j + 1 < nblk);
-    if (j + 2 < nblk) super(PfParity<2>{}, j + 2, false);
+    if (j < nfb) super(PfParity<0>{}, j, j + 1 < nfb);
+    if (j + 2 < nfb) super(PfParity<2>{}, j + 2, false);
+    if (nblk > 0) {
+      wait_vmcnt<0>();                                      // this wave's part of V_{nblk-1} landed
+      ring_barrier();
+      const int st = nfb & 3;
+      last_block(st == 0 ? lv0 : st == 1 ? lv1 : st == 2 ? lv2 : lv3);
+    }
   } else {
     // Two-stage ring, one barrier per block: the barrier before block j
     // retires block j - 1, whose stages block j's QK product refills with
@@ -871,11 +941,16 @@ void prefill_fwd(const PrefillArgs a) {
       load_q();
     }
     int j = 0;
-    for (; j + 1 < nblk; j += 2) {
+    for (; j + 1 < nfb; j += 2) {
       step(PfParity<0>{}, j, s0, s1, n0, n1);
       step(PfParity<1>{}, j + 1, n0, n1, s0, s1);
     }
-    if (j < nblk) step(PfParity<0>{}, j, s0, s1, n0, n1);
+    if (j < nfb) step(PfParity<0>{}, j, s0, s1, n0, n1);
+    if (nblk > 0) {
+      wait_vmcnt<0>();                                      // this wave's part of V_{nblk-1} landed
+      ring_barrier();
+      last_block((nfb & 1) ? lv1 : lv0);
+    }
   }
 
   // ---- normalise and store.  The lane owns query qi, d = 32 e + 8 (j / 4) +
