@@ -84,11 +84,12 @@ def time_decode(pkg, cases, steps: int, warmup: int):
     """Clock settle, W untimed calls, then two timed passes of exactly `steps` calls.
 
     Call i reads input set i % len(cases) (several sets rotate when one set
-    would fit in the 256 MB MALL).  Pass 1: the library records a HIP event
-    on the launch stream just before and just after `decode_main` of every
-    call; main-kernel time = end_i - begin_i, whole-call time = begin_{i+1} -
-    begin_i (plan, main kernel, split-K merge and launch gaps; the last call
-    is closed by one more call's begin).  Pass 2: no events between calls,
+    would fit in the 256 MB MALL).  Pass 1: the library stamps a pair of HIP
+    events with the start and end of `decode_main` of every call (launched
+    through hipExtLaunchKernel, so the events are the dispatch's own
+    timestamps, with no marker packets); main-kernel time = end_i - begin_i,
+    whole-call time = begin_{i+1} - begin_i (main kernel, split-K merge and
+    launch gaps; the last call is closed by one more call's begin).  Pass 2: no events between calls,
     only around the loop: the back-to-back mean per call and the host
     microseconds to issue one call.
     Returns (per-call whole-call ms, per-call main-kernel ms, back-to-back ms, host us).
@@ -214,8 +215,8 @@ def bench_decode_config(pkg, cases, steps, warmup):
         "algorithmic_bytes": nbytes,
         "statistic": (f"GBps and back_to_back: the {steps} timed calls issued back to back between two "
                       "synchronizes (no events between calls); us_per_call: median of a separate pass of "
-                      f"{steps} calls, begin-to-begin of the library's events around decode_main (min "
-                      "alongside; the events add a few microseconds per call)"),
+                      f"{steps} calls, begin-to-begin of the events stamped with decode_main's start (min "
+                      "alongside)"),
     }
 
 
@@ -239,12 +240,15 @@ def bench_prefill_config(pkg, steps: int, warmup: int):
     q, k, v = syn.cfg4(torch.device("cuda:0"))
     B, Hq, T, D = q.shape
     t = time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True), steps, warmup)
-    ms = t["median_ms"]
     flops = syn.prefill_flops(B, Hq, T, D)
-    tf = flops / (ms * 1e-3) / 1e12
+    tf = flops / (t["mean_ms"] * 1e-3) / 1e12
+    tf_med = flops / (t["median_ms"] * 1e-3) / 1e12
     return {**_timing_fields(t), "TFLOPs": round(tf, 1), "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+            "TFLOPs_median_call": round(tf_med, 1),
             "algorithmic_flops": flops, "workload": "config 4: causal prefill bf16 B4 T2048 32/8 heads D128",
-            "statistic": f"median of {steps} calls",
+            "statistic": (f"TFLOPs: the {steps} timed calls issued back to back between two synchronizes (as the "
+                          f"headline's value); TFLOPs_median_call: median of a separate pass of {steps} calls "
+                          "with an event between calls"),
             "rope_prologue": bench_rope_prologue(pkg, q, k, v, steps, warmup)}
 
 
@@ -443,23 +447,27 @@ def bench_qwen35_config(pkg, steps: int, warmup: int):
     v = torch.randn(B, Hkv, S, D, device=dev, generator=g).to(torch.bfloat16)
     kv_len = torch.tensor([S], dtype=torch.int32, device=dev)
     t = time_calls(lambda: pkg.attention_flash_decode(q, k, v, kv_len), steps, warmup)
-    ms = t["median_ms"]
     nbytes = 2 * B * Hkv * S * D * 2 + 2 * B * Hq * D * 2
-    gbs = nbytes / (ms * 1e-3) / 1e9
+    gbs = nbytes / (t["mean_ms"] * 1e-3) / 1e9
     out["decode_B32_ctx4096"] = {**_timing_fields(t), "GBps": round(gbs, 1),
-                                 "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": nbytes}
+                                 "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4),
+                                 "GBps_median_call": round(nbytes / (t["median_ms"] * 1e-3) / 1e9, 1),
+                                 "algorithmic_bytes": nbytes}
     del q, k, v
     T = 4096
     q = (torch.randn(1, Hq, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
     k = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
     v = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.bfloat16)
     t = time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=True), steps, warmup)
-    ms = t["median_ms"]
     flops = _syn().prefill_flops(1, Hq, T, D)
-    tf = flops / (ms * 1e-3) / 1e12
+    tf = flops / (t["mean_ms"] * 1e-3) / 1e12
     out["prefill_B1_T4096"] = {**_timing_fields(t), "TFLOPs": round(tf, 1),
-                               "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4), "algorithmic_flops": flops}
+                               "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+                               "TFLOPs_median_call": round(flops / (t["median_ms"] * 1e-3) / 1e12, 1),
+                               "algorithmic_flops": flops}
     out["workload"] = "Qwen3.5 full attention: head_dim 256, 16/4 heads, bf16, contiguous cache"
+    out["statistic"] = ("GBps / TFLOPs: calls issued back to back between two synchronizes; *_median_call: "
+                        "median of a separate pass with an event between calls")
     return out
 
 
@@ -643,7 +651,7 @@ def main(argv=None):
             "kernel": "decode_main",
             "kernel_us": head["main_kernel_us"],
             "kernel_us_min": head["main_kernel_us_min"],
-            "statistic": "median of the per-call HIP events around decode_main",
+            "statistic": "median of the per-call HIP events stamped with decode_main's start and end",
         },
     }
     tr = load_traffic(f"decode_main_{args.config}")

@@ -69,8 +69,9 @@ typedef struct sia_tensor {
 typedef struct sia_decode_options {
   int32_t tiles_per_split;  /* 0 = automatic; else force this many 16-token tiles per split-K item */
   int32_t reserved0;        /* must be zero */
-  void* main_begin_event;   /* optional hipEvent_t recorded on `stream` just before the main decode kernel */
-  void* main_end_event;     /* optional hipEvent_t recorded just after it (before the split-K reduction) */
+  void* main_begin_event;   /* optional hipEvent_t (created with timing): stamped with the main decode kernel's start */
+  void* main_end_event;     /* optional hipEvent_t: stamped with its end (before the split-K reduction); both through
+                               hipExtLaunchKernel, so the interval is the kernel's own execution */
   int64_t reserved[4];      /* must be zero */
 } sia_decode_options;
 

@@ -270,20 +270,22 @@ static int launch_f32_typed(F32Launch& L) {
   const F32Args& a = L.a;
   const int64_t items = (int64_t)a.B * a.Hkv * a.nchunk * a.nsplit;
   if (items > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "fp32 attention: too many work items");
-  if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
-    return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
-  if (items > 0) hipLaunchKernelGGL((attn_f32<D, QT, KV, ST>), dim3((unsigned)items), dim3(256), 0, L.stream, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "fp32 attention launch: %s", hipGetErrorString(e));
-  if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
-    return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
+  if (items == 0) {   // nothing to launch: the events mark an empty interval
+    if ((L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess) ||
+        (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess))
+      return fail(SIA_ERR_LAUNCH, "cannot record the main kernel's events");
+  } else {
+    const int rc = launch_kernel(attn_f32<D, QT, KV, ST>, dim3((unsigned)items), dim3(256), 0, L.stream,
+                                 L.begin_event, L.end_event, "fp32 attention", a);
+    if (rc != SIA_OK) return rc;
+  }
   if (a.nsplit > 1) {
     constexpr int RPB = 4 * (64 / (D / 4));
     const int64_t rows = (int64_t)a.B * a.Hq * a.Tq;
     const int64_t blocks = (rows + RPB - 1) / RPB;
     if (blocks > 0x7fffffff) return fail(SIA_ERR_UNSUPPORTED, "fp32 attention: too many rows");
     hipLaunchKernelGGL((attn_f32_merge<D, QT>), dim3((unsigned)blocks), dim3(256), 0, L.stream, a);
-    e = hipGetLastError();
+    const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "fp32 attention merge launch: %s", hipGetErrorString(e));
   }
   return SIA_OK;

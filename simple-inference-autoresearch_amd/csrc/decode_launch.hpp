@@ -63,14 +63,9 @@ int launch_decode_typed(DecodeLaunch& L) {
                     L.a.max_items / 2 >= L.a.slots;
   // 1. main (persistent, stream-K share per group), 2. merge of the split
   // pieces (unless direct_only)
-  if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
-    return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
-  hipLaunchKernelGGL(kmain, dim3(L.a.slots), dim3(NW * 64), lds, L.stream, L.a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode launch: %s", hipGetErrorString(e));
-  if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
-    return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
-  if (L.a.direct_only) return SIA_OK;
+  const int rc = launch_kernel(kmain, dim3(L.a.slots), dim3(NW * 64), lds, L.stream, L.begin_event, L.end_event,
+                               "decode", L.a);
+  if (rc != SIA_OK || L.a.direct_only) return rc;
   const int rows = L.a.B * L.a.Hq;
   constexpr int kRowsPerGroup = 64 / (D / 4);
   const int ngroups = (rows + kRowsPerGroup - 1) / kRowsPerGroup;
@@ -79,7 +74,7 @@ int launch_decode_typed(DecodeLaunch& L) {
     hipLaunchKernelGGL((decode_reduce<D, QT, NW, 8>), dim3(ngroups), dim3(8 * 64), 0, L.stream, L.a);
   else
     hipLaunchKernelGGL((decode_reduce<D, QT, NW, 1>), dim3(ngroups), dim3(64), 0, L.stream, L.a);
-  e = hipGetLastError();
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "decode reduce launch: %s", hipGetErrorString(e));
   return SIA_OK;
 }

@@ -151,16 +151,11 @@ int launch_decode_small(DecodeLaunch& L) {
   const int64_t waves = rows * nsplit;
   const dim3 grid((unsigned)((waves + 3) / 4));
   float* part = (float*)L.ws;
-  if (L.begin_event && hipEventRecord(L.begin_event, L.stream) != hipSuccess)
-    return fail(SIA_ERR_LAUNCH, "cannot record main_begin_event");
-  if (L.D == 16)
-    hipLaunchKernelGGL((decode_small<16, KV, QT, ST>), grid, dim3(256), 0, L.stream, L.a, (int)nsplit, (int)tps, part);
-  else
-    hipLaunchKernelGGL((decode_small<32, KV, QT, ST>), grid, dim3(256), 0, L.stream, L.a, (int)nsplit, (int)tps, part);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "small decode launch: %s", hipGetErrorString(e));
-  if (L.end_event && hipEventRecord(L.end_event, L.stream) != hipSuccess)
-    return fail(SIA_ERR_LAUNCH, "cannot record main_end_event");
+  const int rc = L.D == 16 ? launch_kernel(decode_small<16, KV, QT, ST>, grid, dim3(256), 0, L.stream, L.begin_event,
+                                           L.end_event, "small decode", L.a, (int)nsplit, (int)tps, part)
+                           : launch_kernel(decode_small<32, KV, QT, ST>, grid, dim3(256), 0, L.stream, L.begin_event,
+                                           L.end_event, "small decode", L.a, (int)nsplit, (int)tps, part);
+  if (rc != SIA_OK) return rc;
   if (nsplit == 1) return SIA_OK;
   F32Args m;
   memset(&m, 0, sizeof(m));

@@ -1,6 +1,7 @@
 // Host helpers: error reporting, device facts, occupancy cache, tensor checks.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -27,6 +28,22 @@ inline int device_ok() {
   const DeviceInfo& dev = device_info();
   if (dev.id < 0) return fail(SIA_ERR_DEVICE, "no HIP device is current");
   if (!dev.gfx950) return fail(SIA_ERR_DEVICE, "this library is built for gfx950 (MI355X) only");
+  return SIA_OK;
+}
+
+// Launches `kernel` on `stream`.  With timing events it goes through
+// hipExtLaunchKernel, which stamps `begin` and `end` with the kernel's own
+// start and end times (no marker packets around the dispatch, so short
+// kernels are timed as a kernel trace times them).
+template <class K, class... Args>
+int launch_kernel(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, hipEvent_t begin,
+                  hipEvent_t end, const char* what, Args... args) {
+  if (begin || end)
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, begin, end, 0u, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "%s launch: %s", what, hipGetErrorString(e));
   return SIA_OK;
 }
 

@@ -52,9 +52,11 @@ def decode_options(tiles_per_split: int = 0, main_events=None):
     """Options for decode calls made in this block (this thread).
 
     tiles_per_split: force the split-K size in 16-token tiles (0 = automatic).
-    main_events: optional ``(begin, end)`` pair of ``torch.cuda.Event``; the
-        library records them on the launch stream around the main decode
-        kernel (excluding the split-K reduction), for kernel timing.
+    main_events: optional ``(begin, end)`` pair of timing ``torch.cuda.Event``
+        (already recorded once, so that their HIP events exist); the library
+        stamps them with the main decode kernel's own start and end
+        (hipExtLaunchKernel; the split-K reduction is outside), for kernel
+        timing.
     """
     global _opts_users
     prev = (getattr(_tls, "tiles_per_split", 0), getattr(_tls, "main_events", None))
