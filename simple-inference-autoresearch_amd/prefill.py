@@ -26,14 +26,14 @@ def prefill_workspace_size(batch: int, kv_heads: int, kv_len: int, head_dim: int
     return int(_lib.gpu_ops().prefill_workspace_size(batch, kv_heads, kv_len, head_dim))
 
 
-def _supported_view(t: torch.Tensor) -> bool:
-    if t.stride(-1) != 1 or t.data_ptr() % 16:
-        return False
-    es = t.element_size()
-    if not all((s * es) % 16 == 0 for s in t.stride()[:-1]):
-        return False
-    # K/V rows are fetched with 32-bit offsets of up to 64 rows from a block start
-    return t.shape[-2] <= 1 or t.shape[-1] * es <= t.stride(-2) * es < (1 << 31) // 64
+_OPS = None   # the extension module, once loaded on a GPU
+
+
+def _ops():
+    global _OPS
+    if _OPS is None:
+        _OPS = _lib.gpu_ops()
+    return _OPS
 
 
 def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool,
@@ -43,8 +43,9 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
 
     q: (B, Hq, Tq, D); k, v: (B, Hkv, Tk, D); returns (B, Hq, Tq, D), or
     (B, Tq, Hq, D) when ``out_token_major``, in q's dtype.  Strided views are
-    read in place; a view is copied only when its layout cannot be read
-    directly (head_dim not contiguous or rows not 16-byte aligned), so
+    read in place; the extension copies a view only when its layout cannot be
+    read directly (head_dim not contiguous, rows not 16-byte aligned, or rows
+    too far apart for 32-bit offsets within a 64-key block), so
     ``assume_contiguous`` never changes the result.
     """
     B, Hq, Tq, D = q.shape
@@ -55,7 +56,7 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
         raise AssertionError(f"unsupported head_dim {D}")
     if sm_scale is None:
         sm_scale = 1.0 / (D ** 0.5)
-    ops = _lib.gpu_ops()
+    ops = _ops()
     if Tq == 1 and Tk >= 1 and D in _DECODE_DIMS and k.dtype == q.dtype and v.dtype == q.dtype and q.is_cuda:
         # one query row sees every key (bottom-right causal == full at Tq = 1):
         # the decode kernels stream K/V once per KV-head group instead of
@@ -64,7 +65,6 @@ def attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, ca
         kv_len = torch.full((1,), Tk, dtype=torch.int32, device=q.device)
         out = _run(CONTIG, q, k, v, None, None, None, kv_len, 0, float(sm_scale))
         return out if out_token_major else out.view(B, Hq, 1, D)
-    q, k, v = (t if _supported_view(t) else t.contiguous() for t in (q, k, v))
     return ops.prefill(q, k, v, bool(causal), float(sm_scale), bool(out_token_major))
 
 
@@ -101,6 +101,5 @@ def rope_attention_flash_triton(q: torch.Tensor, k: torch.Tensor, v: torch.Tenso
         # the kernel reads tables in q's dtype or fp32; widening the other
         # 16-bit type to fp32 is exact, and the rotation runs in fp32 anyway
         cos, sin = cos.float(), sin.float()
-    q, k, v = (t if _supported_view(t) else t.contiguous() for t in (q, k, v))
-    return _lib.gpu_ops().prefill_rope(q, k, v, cos, sin, bool(interleaved), start_pos, int(start_offset),
+    return _ops().prefill_rope(q, k, v, cos, sin, bool(interleaved), start_pos, int(start_offset),
                                        bool(causal), float(sm_scale), bool(out_token_major))

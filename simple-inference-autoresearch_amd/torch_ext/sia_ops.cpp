@@ -170,11 +170,28 @@ Tensor decode(int64_t kind, const Tensor& q, const Tensor& k, const Tensor& v, c
   return out;
 }
 
+// A prefill operand as the kernels read it: in place when head_dim is
+// contiguous, rows are 16-byte aligned and the rows of one 64-key block lie
+// within 32-bit offsets; any other view is copied.
+Tensor readable(const Tensor& t) {
+  if (t.dim() < 2) return t;
+  const int64_t es = t.element_size();
+  bool ok = t.stride(-1) == 1 && reinterpret_cast<uintptr_t>(t.data_ptr()) % 16 == 0;
+  for (int64_t i = 0; ok && i < t.dim() - 1; ++i) ok = (t.stride(i) * es) % 16 == 0;
+  if (ok && t.size(-2) > 1) {
+    const int64_t row = t.stride(-2) * es;
+    ok = t.size(-1) * es <= row && row < (int64_t(1) << 31) / 64;
+  }
+  return ok ? t : t.contiguous();
+}
+
 // Causal / full attention (q (B, Hq, Tq, D)) -> (B, Hq, Tq, D) or token-major (B, Tq, Hq, D).
-Tensor prefill(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, double sm_scale, bool out_token_major) {
-  const at::Device dev = gpu_of(q, "q");
+Tensor prefill(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, bool causal, double sm_scale,
+               bool out_token_major) {
+  const at::Device dev = gpu_of(q_in, "q");
   const c10::DeviceGuard guard(dev);
-  if (q.dim() != 4 || k.dim() != 4) throw py::value_error("q, k and v must have 4 dims");
+  if (q_in.dim() != 4 || k_in.dim() != 4) throw py::value_error("q, k and v must have 4 dims");
+  const Tensor q = readable(q_in), k = readable(k_in), v = readable(v_in);
   const int64_t B = q.size(0), Hq = q.size(1), Tq = q.size(2), D = q.size(3);
   const int64_t Hkv = k.size(1), Tk = k.size(2);
   const sia_tensor dq = desc(q, dev, "q"), dk = desc(k, dev, "k"), dv = desc(v, dev, "v");
@@ -190,12 +207,13 @@ Tensor prefill(const Tensor& q, const Tensor& k, const Tensor& v, bool causal, d
 }
 
 // prefill with q rotated at load: q (B, Hq, Tq, D) un-rotated, k rotated.
-Tensor prefill_rope(const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& cos, const Tensor& sin,
+Tensor prefill_rope(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, const Tensor& cos, const Tensor& sin,
                     bool interleaved, const OptT& start_pos, int64_t start_offset, bool causal, double sm_scale,
                     bool out_token_major) {
-  const at::Device dev = gpu_of(q, "q");
+  const at::Device dev = gpu_of(q_in, "q");
   const c10::DeviceGuard guard(dev);
-  if (q.dim() != 4 || k.dim() != 4) throw py::value_error("q, k and v must have 4 dims");
+  if (q_in.dim() != 4 || k_in.dim() != 4) throw py::value_error("q, k and v must have 4 dims");
+  const Tensor q = readable(q_in), k = readable(k_in), v = readable(v_in);
   const int64_t B = q.size(0), Hq = q.size(1), Tq = q.size(2), D = q.size(3);
   const int64_t Hkv = k.size(1), Tk = k.size(2);
   const sia_tensor dq = desc(q, dev, "q"), dk = desc(k, dev, "k"), dv = desc(v, dev, "v"),

@@ -83,6 +83,38 @@ def test_strided_views_and_token_major(gpu_pkg):
     check(ref_layout, O.flash_attention(f64(q), f64(k), f64(v), True), "strided")
 
 
+@pytest.mark.parametrize("layout", ["d_strided", "misaligned", "far_rows"])
+def test_views_that_are_copied(gpu_pkg, layout):
+    """Views the kernels cannot read in place are copied by the extension first:
+    head_dim not contiguous, rows not 16-byte aligned, or K/V rows 32 MB apart
+    (the rows of one 64-key block would span 2^31 bytes of 32-bit offsets).
+    Each gives the same bits as the contiguous inputs, and matches the oracle."""
+    announce(f"prefill views copied by the extension: {layout}")
+    B, Hq, Hkv, T, D = (1, 4, 1, 70, 64) if layout == "far_rows" else (1, 8, 2, 100, 64)
+    q, k, v = qkv(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=17)
+    if layout == "d_strided":        # (B, H, D, T) storage, transposed: head_dim has stride T
+        views = [t.transpose(-1, -2).contiguous().transpose(-1, -2) for t in (q, k, v)]
+    elif layout == "misaligned":     # rows start 2 bytes past a 16-byte boundary
+        views = []
+        for t in (q, k, v):
+            base = torch.empty(*t.shape[:-1], D + 1, dtype=t.dtype, device=DEV)
+            base[..., 1:] = t
+            views.append(base[..., 1:])
+    else:                            # one KV head, rows 2^24 elements (32 MB) apart
+        row = 1 << 24
+        views = [q]
+        for t in (k, v):
+            base = torch.empty(T * row, dtype=t.dtype, device=DEV)
+            view = base.as_strided((B, Hkv, T, D), (0, 0, row, 1))
+            view.copy_(t)
+            views.append(view)
+    out = gpu_pkg.attention_flash_triton(*views, causal=True)
+    ref_layout = gpu_pkg.attention_flash_triton(q, k, v, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_layout)
+    check(out, O.flash_attention(f64(q), f64(k), f64(v), True), layout)
+
+
 @pytest.mark.parametrize("Hq,Hkv", [(4, 4), (8, 4), (12, 4), (6, 1), (8, 1), (32, 2), (24, 2)])
 @pytest.mark.parametrize("D", [64, 256])
 @pytest.mark.parametrize("B,causal", [(1, True), (3, False), (2, True)])
