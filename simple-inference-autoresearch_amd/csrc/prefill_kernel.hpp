@@ -60,6 +60,7 @@ struct PrefillArgs {
   const char* q; int64_t q_sb, q_sh, q_sm;     // byte strides; head_dim contiguous
   const char* k; int64_t k_sb, k_sh, k_sn;
   const char* vimg;                             // V^T block images (prefill_pack_v)
+  const char* v; int64_t v_sb, v_sh, v_sn;      // raw V (variant 2: images built in LDS)
   char* out; int64_t o_sb, o_sh, o_sm;
   int32_t B, Hq, Hkv, G, Tq, Tk, causal;
   float qk_scale;                               // sm_scale * log2(e)
@@ -95,6 +96,10 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 //    exceed the CU count, e.g. one sequence of up to 2048 tokens): 4 waves
 //    and a two-stage ring, so twice the work-groups, and a causal work-group
 //    covers half the rows (B1 T = 1024: 30.5 -> 25.6 us per call).
+//    Variant 2 is variant 1 without prefill_pack_v: V blocks come into the
+//    ring as raw rows and every work-group builds the f16 V^T image of each
+//    block in LDS (more vector work per block, one launch less per call;
+//    chosen for short key ranges, where the call is launch- and latency-bound).
 //  * D <= 64: 4 waves with the same register budget, so two work-groups share
 //    a CU and one's prologue and epilogue overlap the other's key loop (MHA
 //    D = 64 at T = 1024: 88 -> 70 us per call); a two-stage ring at D = 64,
@@ -106,7 +111,8 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 // dimensions wide (D = 16 is zero-padded).
 template <int D, int VAR = 0>
 struct PfCfg {
-  static constexpr bool small = VAR == 1;
+  static constexpr bool small = VAR >= 1;
+  static constexpr bool packv = VAR == 2;                 // V^T images built in LDS from raw V rows
   static constexpr int waves = D == 128 && !small ? 8 : 4;
   static constexpr int stages = small ? 2 : D == 128 || D < 64 ? 4 : 2;
   static constexpr int wpe = D <= 128 ? 2 : 1;          // waves per SIMD the registers are budgeted for
@@ -371,11 +377,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // (one template argument each: __launch_bounds__ is a macro)
-template <int C> constexpr int kPfThreads = PfCfg<C / 2, C % 2>::waves * 64;
-template <int C> constexpr int kPfWpe = PfCfg<C / 2, C % 2>::wpe;
+template <int C> constexpr int kPfThreads = PfCfg<C / 4, C % 4>::waves * 64;
+template <int C> constexpr int kPfWpe = PfCfg<C / 4, C % 4>::wpe;
 
 template <int D, class T, int ROPE, int VAR>
-__global__ __launch_bounds__(kPfThreads<2 * D + VAR>) __attribute__((amdgpu_waves_per_eu(kPfWpe<2 * D + VAR>)))
+__global__ __launch_bounds__(kPfThreads<4 * D + VAR>) __attribute__((amdgpu_waves_per_eu(kPfWpe<4 * D + VAR>)))
 void prefill_fwd(const PrefillArgs a) {
   using C = PfCfg<D, VAR>;
   constexpr int NW = C::waves, S = C::stages, DV = C::DV;
@@ -480,6 +486,14 @@ void prefill_fwd(const PrefillArgs a) {
     const int r = (wave * NK + i) * ROWS_PER_DMA + lane / NC;
     k_voff[i] = r * (int)a.k_sn + (((lane % NC) ^ (r % NC)) * 16);
   }
+  // variant 2: raw V rows land in the V stages like K rows (same swizzle)
+  const char* vb = C::packv ? a.v + b * a.v_sb + (int64_t)hkv * a.v_sh : nullptr;
+  int v_voff[NK];
+#pragma unroll
+  for (int i = 0; i < NK; ++i) {
+    const int r = (wave * NK + i) * ROWS_PER_DMA + lane / NC;
+    v_voff[i] = C::packv ? r * (int)a.v_sn + (((lane % NC) ^ (r % NC)) * 16) : 0;
+  }
   // QK operand addresses: k-step j reads chunk 2 j + h of row l32 (tile 0)
   // and row l32 + 32 (tile 1: + 32 RB, same swizzle since 32 % NC == 0)
   int k_rd[KST];
@@ -515,7 +529,17 @@ void prefill_fwd(const PrefillArgs a) {
   };
   auto issue_v1 = [&](int blk, char* LV, int i) {
     const bool live = blk < nblk;
-    {
+    if constexpr (C::packv) {
+      const int key0 = live ? blk * kPfBN : 0;
+      const int rows = live ? min(kPfBN, a.Tk - key0) : 0;
+      const int c = wave * NK + i;
+      const bool real = c < C::kdma;
+      const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+          (void*)(vb + (int64_t)key0 * a.v_sn), 0, real ? rows * (int)a.v_sn : 0, kBufferFlags);
+      const int voff = v_voff[i];
+      char* dst = real ? LV + c * 1024 : ldummy;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, dst, 16, voff, 0, 0, 0);
+    } else {
       const int c = wave * NV + i;
       const bool real = c < C::vdma;
       const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
@@ -533,6 +557,45 @@ void prefill_fwd(const PrefillArgs a) {
   auto issue_v = [&](int blk, char* LV) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) issue_v1(blk, LV, i);
+  };
+  // Variant 2: turn the raw V block of stage LV (key rows, swizzled as the K
+  // stages) into its f16 V^T image, in place.  Every thread gathers 4
+  // dimensions of one 8-key image chunk group (8 LDS reads of 8 bytes); after
+  // a barrier (every raw row read) it writes those 4 image chunks over the
+  // stage, and a second barrier makes the image whole.
+  auto pack_vstage = [&](char* LV) {
+    if constexpr (C::packv) {
+      static_assert(NK == NV && KB == VB && DV == D && NW * 64 == 8 * (D / 4), "variant 2 geometry");
+      __builtin_amdgcn_sched_barrier(0);
+      // (t passes through an empty asm so that the address arithmetic stays
+      // inside this step: hoisted out of the key loop, its registers would be
+      // held across every block)
+      int t = threadIdx.x;
+      asm volatile("" : "+v"(t));
+      const int c = t / (D / 4), d0 = 4 * (t % (D / 4));
+      u32x2 r[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = image_key(c, i);
+        r[i] = *(const u32x2*)(LV + k * RB + (((d0 >> 3) ^ (k % NC)) * 16) + (d0 & 7) * 2);
+      }
+      u32x4 w[4];
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const uint32_t e0 = ((uint32_t)r[2 * m][tt >> 1] >> (16 * (tt & 1))) & 0xffffu;
+          const uint32_t e1 = ((uint32_t)r[2 * m + 1][tt >> 1] >> (16 * (tt & 1))) & 0xffffu;
+          w[tt][m] = elem_f16(T{}, e0) | (elem_f16(T{}, e1) << 16);
+        }
+      ring_barrier();     // every raw row of the stage is read
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) *(u32x4*)(LV + (c * DV + d0 + tt) * 16) = w[tt];
+      ring_barrier();     // the whole image is written before any wave reads it
+      // (nothing of the block step that follows is scheduled into the
+      // conversion, where its registers would add to the pack's)
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   // A work step's ring refill: NP single transfers (K pieces, then V
   // pieces).  On the four-stage ring they are issued from inside the QK
@@ -923,6 +986,7 @@ void prefill_fwd(const PrefillArgs a) {
       ring_barrier();
       issue_k(j + 2, kstage(PfParity<P>{}));             // K_{j+2}, V_{j+1} into the stages retired here
       issue_v(j + 1, vstage(PfParity<P + 1>{}));
+      pack_vstage(vstage(PfParity<P>{}));                // variant 2: V_j's image (its rows have landed)
       work(parity, j, sa0, sa1, sb0, sb1, rmax, no_piece);
     };
     // Prologue as on the four-stage ring: K_0, q, then V_0 and K_1 landing
@@ -949,7 +1013,9 @@ void prefill_fwd(const PrefillArgs a) {
     if (nblk > 0) {
       wait_vmcnt<0>();                                      // this wave's part of V_{nblk-1} landed
       ring_barrier();
-      last_block((nfb & 1) ? lv1 : lv0);
+      char* vlast = (nfb & 1) ? lv1 : lv0;
+      pack_vstage(vlast);   // (variant 2; one copy: a stage picked by a branch here kept the scores on the stack)
+      last_block(vlast);
     }
   }
 
