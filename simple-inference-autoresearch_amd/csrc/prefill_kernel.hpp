@@ -584,9 +584,18 @@ void prefill_fwd(const PrefillArgs a) {
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const uint32_t e0 = ((uint32_t)r[2 * m][tt >> 1] >> (16 * (tt & 1))) & 0xffffu;
-          const uint32_t e1 = ((uint32_t)r[2 * m + 1][tt >> 1] >> (16 * (tt & 1))) & 0xffffu;
-          w[tt][m] = elem_f16(T{}, e0) | (elem_f16(T{}, e1) << 16);
+          const uint32_t x0 = r[2 * m][tt >> 1], x1 = r[2 * m + 1][tt >> 1];
+          if constexpr (std::is_same<T, BF16>::value) {
+            // the bf16 bits as f32 (shift or mask), clamped to the f16 range,
+            // both rounded in one packed conversion: elem_f16's result
+            const float f0 = __builtin_bit_cast(float, (tt & 1) ? (x0 & 0xffff0000u) : (x0 << 16));
+            const float f1 = __builtin_bit_cast(float, (tt & 1) ? (x1 & 0xffff0000u) : (x1 << 16));
+            w[tt][m] = pack2(F16{}, __builtin_amdgcn_fmed3f(f0, -65504.0f, 65504.0f),
+                             __builtin_amdgcn_fmed3f(f1, -65504.0f, 65504.0f));
+          } else {
+            const uint32_t e0 = (x0 >> (16 * (tt & 1))) & 0xffffu, e1 = (x1 >> (16 * (tt & 1))) & 0xffffu;
+            w[tt][m] = e0 | (e1 << 16);
+          }
         }
       ring_barrier();     // every raw row of the stage is read
 #pragma unroll
