@@ -190,6 +190,27 @@ def test_d128_grid_sizes(gpu_pkg, B, Tq, Tk, causal):
     check_every_head(out, q, k, v, causal, f"B={B} Tq={Tq} Tk={Tk}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Tq,Tk,causal,token_major", [(256, 256, True, False), (257, 257, True, True),
+                                                       (40, 256, True, True), (256, 256, False, True),
+                                                       (200, 255, False, False), (300, 64, True, False)])
+def test_short_key_ranges(gpu_pkg, dtype, Tq, Tk, causal, token_major):
+    """head_dim 128 with at most 256 keys on a small grid: each work-group
+    builds the f16 V^T images of its key blocks in LDS from raw V rows (no
+    separate repack launch); 257 keys and up take the repack.  Both sides of
+    the cut-over, chunked rows (Tq < Tk), Tq > Tk, and K/V read in place
+    from token-major (B, T, H, D) storage, every head against the oracle."""
+    announce(f"prefill short key range {dtype} Tq={Tq} Tk={Tk} causal={causal} token_major={token_major}")
+    q, k, v = qkv(2, 16, 4, Tq, Tk, 128, dtype, seed=Tq * 3 + Tk)
+    if token_major:   # (B, T, H, D) storage seen as (B, H, T, D): row stride H*D elements
+        q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    check_every_head(out, q, k, v, causal, f"Tq={Tq} Tk={Tk}")
+    if causal and Tq > Tk:
+        assert torch.all(out[:, :, :Tq - Tk] == 0)
+
+
 @pytest.mark.parametrize("D", [64, 128])
 def test_bf16_v_beyond_f16_range_saturates(gpu_pkg, D):
     """The PV product runs in f16, so bf16 V values beyond the f16 range are
