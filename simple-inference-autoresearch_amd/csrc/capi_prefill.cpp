@@ -11,8 +11,12 @@ using namespace sia;
 namespace {
 
 int check4(const sia_tensor* t, const char* name) {
-  if (t == nullptr || t->data == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "%s is missing", name);
+  if (t == nullptr) return fail(SIA_ERR_INVALID_ARGUMENT, "%s is missing", name);
   if (t->ndim != 4) return fail(SIA_ERR_INVALID_ARGUMENT, "%s must have 4 dims", name);
+  // an empty tensor (no queries, or no keys) may have no data pointer: it is
+  // never read or written
+  const bool empty = t->shape[0] == 0 || t->shape[1] == 0 || t->shape[2] == 0 || t->shape[3] == 0;
+  if (t->data == nullptr && !empty) return fail(SIA_ERR_INVALID_ARGUMENT, "%s is missing", name);
   if (t->stride[3] != 1) return fail(SIA_ERR_INVALID_ARGUMENT, "%s must be contiguous along head_dim", name);
   if (!aligned16(t->data)) return fail(SIA_ERR_INVALID_ARGUMENT, "%s must be 16-byte aligned", name);
   for (int d = 0; d < 3; ++d)

@@ -212,6 +212,27 @@ def test_short_key_ranges(gpu_pkg, dtype, Tq, Tk, causal, token_major):
 
 
 @pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_empty_lengths(gpu_pkg, D, dtype):
+    """No keys: every row sees nothing and is written as zeros, the
+    reference's guard of a fully masked row (kernels/attention_kernel.py:224-226).
+    No queries: an empty output, token-major or not.  (Empty tensors may
+    carry no data pointer.)"""
+    announce(f"prefill empty lengths D={D} {dtype}")
+    q, k, v = qkv(2, 8, 2, 5, 0, D, dtype, seed=3)
+    for causal in (True, False):
+        out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+        torch.cuda.synchronize()
+        assert out.shape == (2, 8, 5, D)
+        assert torch.all(out == 0)
+    q, k, v = qkv(2, 8, 2, 0, 7, D, dtype, seed=4)
+    for tm in (False, True):
+        out = gpu_pkg.attention_flash_triton(q, k, v, causal=True, out_token_major=tm)
+        torch.cuda.synchronize()
+        assert out.shape == ((2, 0, 8, D) if tm else (2, 8, 0, D))
+
+
+@pytest.mark.parametrize("D", [64, 128])
 def test_bf16_v_beyond_f16_range_saturates(gpu_pkg, D):
     """The PV product runs in f16, so bf16 V values beyond the f16 range are
     saturated to +-65504 (the reference keeps bf16's range,
