@@ -127,6 +127,9 @@ Tensor decode(int64_t kind, const Tensor& q, const Tensor& k, const Tensor& v, c
   if (q.dim() != 4) throw py::value_error("q must be (B, Hq, 1, D)");
   if (k.dim() != 4) throw py::value_error("k must have 4 dims");
   const int64_t B = q.size(0), Hq = q.size(1), D = q.size(3), Hkv = k.size(1);
+  // an empty batch has nothing to compute (the reference's launch over a
+  // grid of B * Hq programs does nothing either)
+  if (B == 0) return at::empty({0, 1, Hq, D}, q.options());
   const sia_tensor dq = desc(q, dev, "q"), dk = desc(k, dev, "k"), dv = desc(v, dev, "v");
   const sia_tensor dl = desc(kv_len, dev, "kv_len");
   const OptDesc dks(k_scale, dev, "k_scale"), dvs(v_scale, dev, "v_scale"), dbt(block_table, dev, "block_table");

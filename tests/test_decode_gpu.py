@@ -157,6 +157,28 @@ def test_empty_and_single_token(gpu_pkg):
     assert torch.equal(out[1, 0], want)
 
 
+def test_empty_batch(gpu_pkg):
+    """A batch of no sequences returns an empty (0, 1, Hq, D) output from every
+    decode entry point (the reference's grid of B * Hq programs launches none)."""
+    announce("decode with B = 0")
+    Hq, Hkv, S, D = 8, 2, 32, 128
+    q, k, v, _, _ = contiguous_case(0, Hq, Hkv, S, D, torch.bfloat16, torch.bfloat16, seed=1)
+    _, ki, vi, ks, vs = contiguous_case(0, Hq, Hkv, S, D, torch.int8, torch.bfloat16, seed=1)
+    kl = torch.tensor([5], dtype=torch.int32, device=DEV)
+    pool = torch.zeros(4, Hkv, 16, D, dtype=torch.bfloat16, device=DEV)
+    pool8 = torch.zeros(4, Hkv, 16, D, dtype=torch.int8, device=DEV)
+    sc = torch.ones(4, Hkv, 16, dtype=torch.float32, device=DEV)
+    bt = torch.zeros(0, 2, dtype=torch.int32, device=DEV)
+    outs = [gpu_pkg.attention_flash_decode(q, k, v, kl),
+            gpu_pkg.attention_flash_decode_int8(q, ki, vi, ks, vs, kl),
+            gpu_pkg.gqa_int8_flash_decode(q, ki, vi, ks, vs, kl),
+            gpu_pkg.paged_attention_flash_decode(q, pool, pool, bt, kl, 16),
+            gpu_pkg.paged_gqa_int8_flash_decode(q, pool8, pool8, sc, sc, bt, kl, 16)]
+    torch.cuda.synchronize()
+    for o in outs:
+        assert o.shape == (0, 1, Hq, D) and o.dtype == q.dtype
+
+
 @pytest.mark.parametrize("Hq,Hkv", [(64, 2), (64, 8), (48, 1), (32, 32)])
 def test_head_groupings(gpu_pkg, Hq, Hkv):
     announce(f"head grouping Hq={Hq} Hkv={Hkv}")
