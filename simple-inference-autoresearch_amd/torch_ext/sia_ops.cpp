@@ -237,11 +237,12 @@ Tensor prefill_rope(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, 
 std::tuple<Tensor, Tensor> quantize_kv_int8(const Tensor& x, bool scale_f32) {
   const at::Device dev = gpu_of(x, "x");
   const c10::DeviceGuard guard(dev);
-  const sia_tensor dx = desc(x, dev, "x");
   Tensor xi = at::empty(x.sizes(), x.options().dtype(at::kChar));
   std::vector<int64_t> ss(x.sizes().begin(), x.sizes().end());
   if (!ss.empty()) ss.pop_back();
   Tensor scale = at::empty(ss, x.options().dtype(scale_f32 ? at::kFloat : at::kHalf));
+  if (x.numel() == 0 && x.dim() >= 1) return {xi, scale};   // nothing to quantise (empty tensors have no data)
+  const sia_tensor dx = desc(x, dev, "x");
   const sia_tensor dxi = desc(xi, dev, "out"), ds = desc(scale, dev, "scale");
   check(sia_quantize_kv_int8(&dx, &dxi, &ds, stream_of(dev)));
   return {xi, scale};
@@ -252,6 +253,7 @@ void kv_write(const Tensor& k, const OptT& v, const Tensor& k_dst, const OptT& v
               int64_t page_size) {
   const at::Device dev = gpu_of(k, "k");
   const c10::DeviceGuard guard(dev);
+  if (k.numel() == 0 && k.dim() == 4) return;   // no tokens to write
   const sia_tensor dk = desc(k, dev, "k"), dkd = desc(k_dst, dev, "k_dst");
   const OptDesc dv(v, dev, "v"), dvd(v_dst, dev, "v_dst"), dks(k_scale_dst, dev, "k_scale_dst"),
       dvs(v_scale_dst, dev, "v_scale_dst"), dbt(block_table, dev, "block_table"), dsp(start_pos, dev, "start_pos");
@@ -267,6 +269,7 @@ OptT rope_kv_write(const OptT& q, const Tensor& k, const OptT& v, const Tensor& 
   const c10::DeviceGuard guard(dev);
   OptT qo = q_out;
   if (q.has_value() && !qo.has_value()) qo = at::empty(q->sizes(), q->options());
+  if (k.numel() == 0 && k.dim() == 4 && (!q.has_value() || q->numel() == 0)) return qo;   // no tokens
   const sia_tensor dk = desc(k, dev, "k"), dc = desc(cos, dev, "cos"), dsn = desc(sin, dev, "sin"),
                    dkd = desc(k_dst, dev, "k_dst");
   const OptDesc dq(q, dev, "q"), dv(v, dev, "v"), dqo(qo, dev, "q_out"), dvd(v_dst, dev, "v_dst"),
@@ -298,6 +301,7 @@ std::tuple<Tensor, Tensor> rope_qk(const Tensor& q_in, const Tensor& k_in, const
                    dsn = desc(sin, dev, "sin");
   Tensor qo = at::empty(q.sizes(), q.options());
   Tensor ko = at::empty(k.sizes(), k.options());
+  if (q.numel() == 0 && k.numel() == 0 && q.dim() == 4 && k.dim() == 4) return {qo, ko};   // no tokens
   const sia_tensor dqo = desc(qo, dev, "q_out"), dko = desc(ko, dev, "k_out");
   check(sia_rope_qk(&dq, &dk, &dc, &dsn, interleaved ? 1 : 0, &dqo, &dko, stream_of(dev)));
   return {qo, ko};

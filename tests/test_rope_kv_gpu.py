@@ -299,6 +299,27 @@ def test_invalid_arguments(gpu_pkg):
     assert not kc8.any()
 
 
+def test_no_tokens(gpu_pkg):
+    """Zero tokens (T = 0, empty tensors without a data pointer): RoPE returns
+    empty rotations, the cache writes leave the cache untouched and the int8
+    quantiser returns empty outputs, as the reference's empty grids and
+    tensor ops do."""
+    announce("rope / kv write / quantise with no tokens")
+    q, k, v = qkv_slices(2, 0, 4, 2, 64, torch.bfloat16, seed=2)
+    cos, sin = tables(8, 64, torch.bfloat16)
+    qr, kr = gpu_pkg.rope_triton(q, k, cos, sin)
+    assert qr.shape == q.shape and kr.shape == k.shape
+    kc = torch.full((2, 2, 8, 64), 7.0, dtype=torch.bfloat16, device=DEV)
+    vc = kc.clone()
+    qo = gpu_pkg.rope_kv_write(q, k, v, cos, sin, kc, vc, start_offset=3)
+    assert qo.shape == q.shape
+    gpu_pkg.kv_write(k.transpose(1, 2), v.transpose(1, 2), kc, vc)
+    xi, sc = gpu_pkg.quantize_kv_int8(torch.empty(0, 2, 64, dtype=torch.bfloat16, device=DEV))
+    torch.cuda.synchronize()
+    assert torch.all(kc == 7.0) and torch.all(vc == 7.0)
+    assert xi.shape == (0, 2, 64) and xi.dtype == torch.int8 and sc.shape == (0, 2)
+
+
 def test_rope_decode_step_hip_graph_contiguous(gpu_pkg):
     """ops/attention.py:180-245 as one captured graph: fused RoPE + int8 write + attention,
     replayed at new per-sequence positions (ctx filled between replays, as
