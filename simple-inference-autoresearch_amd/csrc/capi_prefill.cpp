@@ -201,6 +201,13 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   a.dHkv = make_fastdiv((uint32_t)Hkv);
   if (rope != nullptr && (rc = setup_rope(*rope, B, Tq, D, q->dtype, a))) return rc;
 
+  // Variant 1 runs two work-groups per CU: a grid of one to two per CU is
+  // resident at once and is folded so that each CU holds a heavy and a light
+  // one (B1 x 2048 tokens: the first CU otherwise holds the two heaviest
+  // causal query blocks' work against half of that on the last).
+  const int64_t nall = (int64_t)a.nqblk * nunit;
+  a.fold = L.var == 1 && dev.cus % 8 == 0 && nall > dev.cus && nall <= 2 * (int64_t)dev.cus ? dev.cus : 0;
+
   PackArgs& p = L.pack;
   p.v = (const char*)v->data; p.v_sb = bstride(v, 0); p.v_sh = bstride(v, 1); p.v_sn = bstride(v, 2);
   p.vimg = (char*)workspace;

@@ -69,6 +69,7 @@ struct PrefillArgs {
   int32_t hpw_lg;                               // log2 of the query heads per work-group (hpw)
   int32_t nunit;                                // work-groups per query block: B * Hkv * (G / hpw)
   int32_t remap;                                // XCD-aware block order (nunit % 8 == 0)
+  int32_t fold;                                 // CU count when the grid fills two work-groups per CU, else 0
   FastDiv dU, dU8, dBH, dHkv;                   // divisions by nunit, nunit / 8, B * Hkv, Hkv
   // rotary embedding of q at load (prefill_fwd<D, T, true> only): query row
   // i of sequence b sits at position start_host + start_pos[b or 0] + i
@@ -413,14 +414,23 @@ void prefill_fwd(const PrefillArgs a) {
   // KV head) lands on one XCD when B * Hkv % 8 == 0.
   // (both orders computed and one selected: a branch here made the compiler
   // load the kernel arguments in four dependent rounds instead of two)
+  // A grid of more work-groups than CUs but at most two per CU is resident
+  // at once: the first `fold` work-groups take one slot of every CU, and
+  // work-group fold + i the second slot of work-group i's CU.  Those are
+  // numbered lightest-first, so every CU pairs a heavy and a light group
+  // (per XCD with the XCD-aware order, whose slots fold the same way).
   int ql, u;
   {
     const int lin = blockIdx.x;
-    const int xcd = lin & 7, slot = lin >> 3;
+    const int nall = a.nqblk * a.nunit;
+    const int xcd = lin & 7;
+    const int slot0 = lin >> 3, f8 = a.fold >> 3;
+    const int slot = a.fold && slot0 >= f8 ? f8 + ((nall >> 3) - 1 - slot0) : slot0;
+    const int lin1 = a.fold && lin >= a.fold ? a.fold + (nall - 1 - lin) : lin;
     const int ql8 = fdiv(slot, a.dU8);
     const int u8 = xcd + 8 * (slot - ql8 * (a.nunit >> 3));
-    const int ql1 = fdiv(lin, a.dU);
-    const int u1 = lin - ql1 * a.nunit;
+    const int ql1 = fdiv(lin1, a.dU);
+    const int u1 = lin1 - ql1 * a.nunit;
     ql = a.remap ? ql8 : ql1;
     u = a.remap ? u8 : u1;
   }

@@ -175,11 +175,15 @@ def test_cfg4_full_size(gpu_pkg):
     print(f"cfg4 max abs err over all 128 heads: {worst:.3e}")
 
 
-@pytest.mark.parametrize("B,Tq,Tk,causal", [(2, 2100, 2100, True), (4, 600, 2500, True), (2, 1500, 1700, False)])
+@pytest.mark.parametrize("B,Tq,Tk,causal", [(2, 2100, 2100, True), (4, 600, 2500, True), (2, 1500, 1700, False),
+                                            (1, 2048, 2048, True), (1, 1500, 1700, False)])
 def test_d128_grid_sizes(gpu_pkg, B, Tq, Tk, causal):
     """head_dim 128 runs 8-wave work-groups when the grid of them exceeds the
-    CU count (these shapes; the small shapes of the other tests run 4-wave
-    groups): ragged and offset lengths, every head against the oracle."""
+    CU count (the first three shapes; the small shapes of the other tests run
+    4-wave groups).  One sequence of 2048 or 1500 rows runs 4-wave groups,
+    more than one per CU and at most two: their order is folded so that each
+    CU holds a heavy and a light one.  Ragged and offset lengths, every head
+    against the oracle."""
     announce(f"prefill D=128 B={B} Tq={Tq} Tk={Tk} causal={causal}")
     g = torch.Generator(device=DEV).manual_seed(Tq + Tk)
     q = (torch.randn(B, 32, Tq, 128, generator=g, device=DEV) * 0.5).to(torch.bfloat16)
