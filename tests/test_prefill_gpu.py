@@ -194,6 +194,18 @@ def test_d128_grid_sizes(gpu_pkg, B, Tq, Tk, causal):
     check_every_head(out, q, k, v, causal, f"B={B} Tq={Tq} Tk={Tk}")
 
 
+@pytest.mark.parametrize("causal", [True, False])
+def test_folded_order_without_xcd_remap(gpu_pkg, causal):
+    """A folded 4-wave grid whose unit count (6) is not a multiple of 8, so the
+    work-groups are folded in linear order rather than per XCD: one sequence
+    of 1500 rows at 24/6 heads (282 work-groups), every head against the oracle."""
+    announce(f"prefill folded linear order causal={causal}")
+    q, k, v = qkv(1, 24, 6, 1500, 1500, 128, torch.bfloat16, seed=77 + causal)
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    check_every_head(out, q, k, v, causal, "24/6 T=1500")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("Tq,Tk,causal,token_major", [(256, 256, True, False), (257, 257, True, True),
                                                        (40, 256, True, True), (256, 256, False, True),
