@@ -214,9 +214,9 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   p.Hkv = (int)Hkv; p.Tk = (int)Tk; p.nkb = a.nkb;
   p.nblocks = B * Hkv * a.nkb;
   // Short key ranges on the 4-wave variant whose grid fits the CUs once:
-  // V^T images built in LDS by each work-group (variant 2, one work-group
-  // per CU for its LDS) instead of by prefill_pack_v, one launch less.  The
-  // raw V rows take the K rows' path (32-bit offsets within a block).
+  // every work-group builds the V^T images of its key blocks in LDS
+  // (variant 2) instead of prefill_pack_v building them, one launch less.
+  // The raw V rows take the K rows' path (32-bit offsets within a block).
   const int64_t v_sn = p.v_sn;
   if (L.var == 1 && rope == nullptr && Tk <= kPackvMaxKeys && (int64_t)a.nqblk * nunit <= dev.cus &&
       (Tk <= 1 || (v_sn >= 2 * D && v_sn * kPfBN < ((int64_t)1 << 31)))) {
