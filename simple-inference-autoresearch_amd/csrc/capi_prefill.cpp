@@ -218,8 +218,17 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   // (variant 2) instead of prefill_pack_v building them, one launch less.
   // The raw V rows take the K rows' path (32-bit offsets within a block).
   const int64_t v_sn = p.v_sn;
-  if (L.var == 1 && rope == nullptr && Tk <= kPackvMaxKeys && (int64_t)a.nqblk * nunit <= dev.cus &&
-      (Tk <= 1 || (v_sn >= 2 * D && v_sn * kPfBN < ((int64_t)1 << 31)))) {
+  const bool v_rows_ok = Tk <= 1 || (v_sn >= 2 * D && v_sn * kPfBN < ((int64_t)1 << 31));
+  if (q->dtype == SIA_F16 && D == 128) {
+    // float16 V needs no conversion: every variant takes raw V rows and reads
+    // them transposed from LDS (no V^T images, no repack)
+    if (!v_rows_ok)
+      return fail(SIA_ERR_UNSUPPORTED, "v token stride %lld bytes: expected [%lld, 2^31/64)", (long long)v_sn,
+                  (long long)(2 * D));
+    a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
+    p.nblocks = 0;
+  } else if (L.var == 1 && rope == nullptr && Tk <= kPackvMaxKeys && (int64_t)a.nqblk * nunit <= dev.cus &&
+             v_rows_ok) {
     L.var = 2;
     a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
     p.nblocks = 0;   // no separate repack

@@ -101,6 +101,8 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 //    ring as raw rows and every work-group builds the f16 V^T image of each
 //    block in LDS (more vector work per block, one launch less per call;
 //    chosen for short key ranges, where the call is launch- and latency-bound).
+//    float16 at D = 128 needs no V^T images in any variant: raw V rows and
+//    transposed LDS reads (kTrV in prefill_fwd).
 //  * D <= 64: 4 waves with the same register budget, so two work-groups share
 //    a CU and one's prologue and epilogue overlap the other's key loop (MHA
 //    D = 64 at T = 1024: 88 -> 70 us per call); a two-stage ring at D = 64,
@@ -391,6 +393,14 @@ void prefill_fwd(const PrefillArgs a) {
   constexpr int KB = C::kblk, VB = C::vblk;
   constexpr int NK = C::kper, NV = C::vper;     // DMA instructions per wave per block
   static_assert(S == 2 || S == 4, "ring depth");
+  // float16 at D = 128: V needs no conversion, so its blocks come into the
+  // ring as raw rows and the PV product reads its A operand with transposed
+  // LDS reads (ds_read_b64_tr_b16) instead of from V^T images: no
+  // prefill_pack_v launch.  (bfloat16 V is converted to float16 for the PV
+  // product, which keeps P at 11 significant bits; a bfloat16 P misses the
+  // 2e-3 output bar.)
+  constexpr bool kTrV = std::is_same<T, F16>::value && D == 128;
+  constexpr bool kRawV = C::packv || kTrV;      // raw V rows in the V stages
   // K stages: swizzled row-major (below); V^T image chunk c of dimension d at
   // c * D * 16 + d * 16
   // (distinct arrays per stage: the compiler then sees that a DMA into one
@@ -496,14 +506,45 @@ void prefill_fwd(const PrefillArgs a) {
     const int r = (wave * NK + i) * ROWS_PER_DMA + lane / NC;
     k_voff[i] = r * (int)a.k_sn + (((lane % NC) ^ (r % NC)) * 16);
   }
-  // variant 2: raw V rows land in the V stages like K rows (same swizzle)
-  const char* vb = C::packv ? a.v + b * a.v_sb + (int64_t)hkv * a.v_sh : nullptr;
+  // raw V rows land in the V stages like K rows.  Variant 2 uses the K
+  // swizzle.  The transposed reads (kTrV) use slot c ^ (4 (r % 4) + (r / 4) % 2)
+  // instead: one such read takes 32 dimensions (4 chunks) of 8 consecutive
+  // rows, and with the K swizzle those 32 chunk reads would share 8 of a
+  // row's 16 bank groups (4-way conflicts); this one spreads them over all 16.
+  auto vswz = [](int r) { return kTrV ? 4 * (r & 3) + ((r >> 2) & 1) : r % NC; };
+  const char* vb = kRawV ? a.v + b * a.v_sb + (int64_t)hkv * a.v_sh : nullptr;
   int v_voff[NK];
 #pragma unroll
   for (int i = 0; i < NK; ++i) {
     const int r = (wave * NK + i) * ROWS_PER_DMA + lane / NC;
-    v_voff[i] = C::packv ? r * (int)a.v_sn + (((lane % NC) ^ (r % NC)) * 16) : 0;
+    v_voff[i] = kRawV ? r * (int)a.v_sn + (((lane % NC) ^ vswz(r)) * 16) : 0;
   }
+  // kTrV: lane L of each 16-lane group gives the address of key row
+  // (L % 16) / 4 of the group's 4 and dimensions 4 (L % 4) .. + 4 of its 16;
+  // the read returns to lane L dimension L % 16 of the group at those 4 keys.
+  // Groups (L / 16) cover dimensions 16 ((L / 16) % 2) of the d-tile and
+  // keys 4 h, so lane (l32, h) gets dimension l32 of the tile at keys
+  // 4 h + [0, 4) of the k-slot (+ 8 for the second read): the image order.
+  // v_tr[e]: this lane's address for d-tile e within the first 16 keys.
+  int v_tr[kTrV ? ET : 1];
+  if constexpr (kTrV) {
+    const int trk = (lane & 15) >> 2, trj = lane & 3, trx = 2 * ((lane >> 4) & 1) + (trj >> 1);
+#pragma unroll
+    for (int e = 0; e < ET; ++e) v_tr[e] = (4 * h + trk) * RB + ((4 * (e ^ trk) + (trx ^ h)) * 16) + 8 * (trj & 1);
+  }
+  // A operand of PV slot x (k-slot x / ET, d-tile x % ET) from V stage Vst:
+  // one V^T image chunk, or two transposed reads of raw rows (kTrV)
+  auto pv_a = [&](const char* Vst, int x) -> u32x4 {
+    if constexpr (kTrV) {
+      typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+      const char* p = Vst + v_tr[x % ET] + (x / ET) * 16 * RB;
+      const u32x2 lo = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)p));
+      const u32x2 hi = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 8 * RB)));
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    } else {
+      return *(const u32x4*)(Vst + h * DV * 16 + l32 * 16 + (x / ET) * 2 * DV * 16 + (x % ET) * 512);
+    }
+  };
   // QK operand addresses: k-step j reads chunk 2 j + h of row l32 (tile 0)
   // and row l32 + 32 (tile 1: + 32 RB, same swizzle since 32 % NC == 0)
   int k_rd[KST];
@@ -539,7 +580,7 @@ void prefill_fwd(const PrefillArgs a) {
   };
   auto issue_v1 = [&](int blk, char* LV, int i) {
     const bool live = blk < nblk;
-    if constexpr (C::packv) {
+    if constexpr (kRawV) {
       const int key0 = live ? blk * kPfBN : 0;
       const int rows = live ? min(kPfBN, a.Tk - key0) : 0;
       const int c = wave * NK + i;
@@ -574,7 +615,7 @@ void prefill_fwd(const PrefillArgs a) {
   // a barrier (every raw row read) it writes those 4 image chunks over the
   // stage, and a second barrier makes the image whole.
   auto pack_vstage = [&](char* LV) {
-    if constexpr (C::packv) {
+    if constexpr (C::packv && !kTrV) {
       static_assert(NK == NV && KB == VB && DV == D && NW * 64 == 8 * (D / 4), "variant 2 geometry");
       __builtin_amdgcn_sched_barrier(0);
       // (t passes through an empty asm so that the address arithmetic stays
@@ -723,13 +764,12 @@ void prefill_fwd(const PrefillArgs a) {
       // holds another block or stale keys and the scores are discarded):
       // one code path keeps the accumulators in place across iterations
       const char* K = kstage(PfParity<P + 1>{});
-      const char* V = vstage(PfParity<P>{}) + h * DV * 16 + l32 * 16;
+      const char* Vst = vstage(PfParity<P>{});
       // A operand of slot i: K rows (k-step i / 2, tile i % 2), then V^T
       // chunks (k-slot x / ET, d-tile x % ET)
       auto rd = [&](int i) -> u32x4 {
         if (i < NQK) return *(const u32x4*)(K + k_rd[i >> 1] + (i & 1) * 32 * RB);
-        const int x = i - NQK;
-        return *(const u32x4*)(V + (x / ET) * 2 * DV * 16 + (x % ET) * 512);
+        return pv_a(Vst, i - NQK);
       };
       const float mu = m == -INFINITY ? 0.f : m;           // rows with nothing visible yet
       const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
@@ -795,7 +835,10 @@ void prefill_fwd(const PrefillArgs a) {
 #pragma unroll
       for (int i = 0; i < NS; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (i + PD < NS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        if (i + PD < NS) {
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+          if (kTrV && i + PD >= NQK) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // (two transposed reads)
+        }
         if (kInlineRefill && i < NQK && (i & 1)) {
 #pragma unroll
           for (int p = 0; p < NP; ++p)
@@ -841,7 +884,6 @@ void prefill_fwd(const PrefillArgs a) {
   auto work_last = [&](const char* Vstage, int j, const f32x16& sa0, const f32x16& sa1) {
     if (j >= wblk) return;
     raise_max(rmax);
-    const char* V = Vstage + h * DV * 16 + l32 * 16;
     const float mu = m == -INFINITY ? 0.f : m;
     const f16x2 ones = {(_Float16)1.0f, (_Float16)1.0f};
     u32x4 pop[4];
@@ -860,7 +902,7 @@ void prefill_fwd(const PrefillArgs a) {
         pop[ks][i] = w;
       }
     };
-    auto rdv = [&](int x) { return *(const u32x4*)(V + (x / ET) * 2 * DV * 16 + (x % ET) * 512); };
+    auto rdv = [&](int x) { return pv_a(Vstage, x); };
     auto pv = [&](auto nks) {
       constexpr int NX = decltype(nks)::value * ET;
       u32x4 buf[3];

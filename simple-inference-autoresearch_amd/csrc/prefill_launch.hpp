@@ -15,7 +15,8 @@ struct PrefillLaunch {
   hipStream_t stream;
 };
 
-// Longest key range that runs variant 2.  The in-LDS conversion costs a
+// Longest key range that runs variant 2 (bfloat16: float16 at D = 128 reads
+// raw V rows at every length and never repacks).  The in-LDS conversion costs a
 // work-group ~0.65 us per 64-key block, the separate repack ~3 us per call
 // (its launch and one load/store round trip): one sequence of 128 tokens
 // 9.8 -> 8.1 us per call, but 512 tokens 15.7 -> 18.1 and 1024 24.0 -> 31.0.

@@ -206,14 +206,33 @@ def test_folded_order_without_xcd_remap(gpu_pkg, causal):
     check_every_head(out, q, k, v, causal, "24/6 T=1500")
 
 
+@pytest.mark.parametrize("B,Tq,Tk,causal,token_major", [(2, 1100, 1100, True, True), (2, 1100, 1100, False, False),
+                                                         (3, 700, 1000, True, False), (1, 1000, 777, False, True),
+                                                         (1, 130, 130, True, True)])
+def test_f16_raw_v_rows(gpu_pkg, B, Tq, Tk, causal, token_major):
+    """float16 at head_dim 128 reads raw V rows with transposed LDS reads (no
+    V^T images, no repack launch), on the 8-wave grid (2 x 1100 rows: 288
+    work-groups) and the 4-wave ones: ragged last key blocks, Tq != Tk, and
+    token-major (B, T, H, D) storage read in place; every head against the
+    oracle."""
+    announce(f"prefill f16 raw V B={B} Tq={Tq} Tk={Tk} causal={causal} token_major={token_major}")
+    q, k, v = qkv(B, 32, 8, Tq, Tk, 128, torch.float16, seed=Tq + 7 * Tk + causal)
+    if token_major:
+        q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    check_every_head(out, q, k, v, causal, f"f16 raw V Tq={Tq} Tk={Tk}")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("Tq,Tk,causal,token_major", [(256, 256, True, False), (257, 257, True, True),
                                                        (40, 256, True, True), (256, 256, False, True),
                                                        (200, 255, False, False), (300, 64, True, False)])
 def test_short_key_ranges(gpu_pkg, dtype, Tq, Tk, causal, token_major):
-    """head_dim 128 with at most 256 keys on a small grid: each work-group
-    builds the f16 V^T images of its key blocks in LDS from raw V rows (no
-    separate repack launch); 257 keys and up take the repack.  Both sides of
+    """head_dim 128 with at most 256 keys on a small grid: with bfloat16 each
+    work-group builds the f16 V^T images of its key blocks in LDS from raw V
+    rows (no separate repack launch); 257 keys and up take the repack (float16
+    reads raw V rows at every length).  Both sides of
     the cut-over, chunked rows (Tq < Tk), Tq > Tk, and K/V read in place
     from token-major (B, T, H, D) storage, every head against the oracle."""
     announce(f"prefill short key range {dtype} Tq={Tq} Tk={Tk} causal={causal} token_major={token_major}")
