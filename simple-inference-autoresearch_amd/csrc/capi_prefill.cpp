@@ -219,7 +219,7 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   // The raw V rows take the K rows' path (32-bit offsets within a block).
   const int64_t v_sn = p.v_sn;
   const bool v_rows_ok = Tk <= 1 || (v_sn >= 2 * D && v_sn * kPfBN < ((int64_t)1 << 31));
-  if (q->dtype == SIA_F16 && D == 128) {
+  if (q->dtype == SIA_F16 && D >= 32 && D <= 128) {
     // float16 V needs no conversion: every variant takes raw V rows and reads
     // them transposed from LDS (no V^T images, no repack)
     if (!v_rows_ok)

@@ -101,8 +101,8 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 //    ring as raw rows and every work-group builds the f16 V^T image of each
 //    block in LDS (more vector work per block, one launch less per call;
 //    chosen for short key ranges, where the call is launch- and latency-bound).
-//    float16 at D = 128 needs no V^T images in any variant: raw V rows and
-//    transposed LDS reads (kTrV in prefill_fwd).
+//    float16 at D = 32 ... 128 needs no V^T images in any variant: raw V rows
+//    and transposed LDS reads (kTrV in prefill_fwd).
 //  * D <= 64: 4 waves with the same register budget, so two work-groups share
 //    a CU and one's prologue and epilogue overlap the other's key loop (MHA
 //    D = 64 at T = 1024: 88 -> 70 us per call); a two-stage ring at D = 64,
@@ -393,13 +393,15 @@ void prefill_fwd(const PrefillArgs a) {
   constexpr int KB = C::kblk, VB = C::vblk;
   constexpr int NK = C::kper, NV = C::vper;     // DMA instructions per wave per block
   static_assert(S == 2 || S == 4, "ring depth");
-  // float16 at D = 128: V needs no conversion, so its blocks come into the
-  // ring as raw rows and the PV product reads its A operand with transposed
-  // LDS reads (ds_read_b64_tr_b16) instead of from V^T images: no
+  // float16 at D = 32 ... 128: V needs no conversion, so its blocks come
+  // into the ring as raw rows and the PV product reads its A operand with
+  // transposed LDS reads (ds_read_b64_tr_b16) instead of from V^T images: no
   // prefill_pack_v launch.  (bfloat16 V is converted to float16 for the PV
   // product, which keeps P at 11 significant bits; a bfloat16 P misses the
-  // 2e-3 output bar.)
-  constexpr bool kTrV = std::is_same<T, F16>::value && D == 128;
+  // 2e-3 output bar.  D = 16 keeps the images, zero-padded to the 32-wide PV
+  // tile.  D = 256, one wave per SIMD, lost 11% to the two reads per operand
+  // against the repack's one launch.)
+  constexpr bool kTrV = std::is_same<T, F16>::value && D >= 32 && D <= 128;
   constexpr bool kRawV = C::packv || kTrV;      // raw V rows in the V stages
   // K stages: swizzled row-major (below); V^T image chunk c of dimension d at
   // c * D * 16 + d * 16
@@ -507,11 +509,20 @@ void prefill_fwd(const PrefillArgs a) {
     k_voff[i] = r * (int)a.k_sn + (((lane % NC) ^ (r % NC)) * 16);
   }
   // raw V rows land in the V stages like K rows.  Variant 2 uses the K
-  // swizzle.  The transposed reads (kTrV) use slot c ^ (4 (r % 4) + (r / 4) % 2)
-  // instead: one such read takes 32 dimensions (4 chunks) of 8 consecutive
-  // rows, and with the K swizzle those 32 chunk reads would share 8 of a
-  // row's 16 bank groups (4-way conflicts); this one spreads them over all 16.
-  auto vswz = [](int r) { return kTrV ? 4 * (r & 3) + ((r >> 2) & 1) : r % NC; };
+  // swizzle.  The transposed reads (kTrV) use their own: one such read takes
+  // 32 dimensions (4 chunks) of 8 consecutive rows, 32 chunk reads that
+  // should cover the 16 chunk-wide bank groups of a 256-byte bank sweep twice
+  // each.  Rows of 256 bytes (D = 128) start a sweep each, and slot
+  // c ^ (4 (r % 4) + (r / 4) % 2) spreads them (the K swizzle, c ^ r % 16,
+  // would put them on 8 groups: 4-way conflicts); 128-byte rows (D = 64)
+  // share a sweep in pairs and take c ^ 4 ((r / 2) % 2); 64-byte rows
+  // (D = 32) already cover a sweep in 4 rows.
+  auto vswz = [](int r) -> int {
+    if constexpr (!kTrV) return r % NC;
+    else if constexpr (NC >= 16) return 4 * (r & 3) + ((r >> 2) & 1);
+    else if constexpr (NC == 8) return 4 * ((r >> 1) & 1);
+    else return 0;
+  };
   const char* vb = kRawV ? a.v + b * a.v_sb + (int64_t)hkv * a.v_sh : nullptr;
   int v_voff[NK];
 #pragma unroll
@@ -525,12 +536,20 @@ void prefill_fwd(const PrefillArgs a) {
   // Groups (L / 16) cover dimensions 16 ((L / 16) % 2) of the d-tile and
   // keys 4 h, so lane (l32, h) gets dimension l32 of the tile at keys
   // 4 h + [0, 4) of the k-slot (+ 8 for the second read): the image order.
-  // v_tr[e]: this lane's address for d-tile e within the first 16 keys.
+  // v_tr[e]: this lane's address for d-tile e within the first 16 keys (the
+  // swizzle depends on the row's low 3 bits only, which k-slot and second
+  // read, +16 and +8 rows, leave alone).
   int v_tr[kTrV ? ET : 1];
   if constexpr (kTrV) {
     const int trk = (lane & 15) >> 2, trj = lane & 3, trx = 2 * ((lane >> 4) & 1) + (trj >> 1);
+    const int row = 4 * h + trk, f = vswz(row);
 #pragma unroll
-    for (int e = 0; e < ET; ++e) v_tr[e] = (4 * h + trk) * RB + ((4 * (e ^ trk) + (trx ^ h)) * 16) + 8 * (trj & 1);
+    for (int e = 0; e < ET; ++e) {
+      v_tr[e] = row * RB + (((4 * e + trx) ^ f) * 16) + 8 * (trj & 1);
+      // (held whole: split into a row part and a chunk part, each read paid
+      // a v_or to join them, 32 per block step)
+      asm volatile("" : "+v"(v_tr[e]));
+    }
   }
   // A operand of PV slot x (k-slot x / ET, d-tile x % ET) from V stage Vst:
   // one V^T image chunk, or two transposed reads of raw rows (kTrV)
