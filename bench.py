@@ -485,8 +485,9 @@ def bench_small_config(pkg, steps: int, warmup: int):
     """One sequence at a time (Llama-3.1-8B attention shapes: 32/8 heads, head_dim 128,
     bf16): causal prefill at the reference's own benchmark lengths
     (benchmarks/benchmark_kernel/bench_attention_compare.py:99-105, B1, T 128 .. 4096),
-    and decode over a contiguous cache of 8192 and 32768 tokens (bf16, and int8 with
-    the fp16 scales of the reference's KVCache)."""
+    the same prefill in fp16 at T 512 and 2048 (same 2.5 PFLOP/s dense peak), and
+    decode over a contiguous cache of 8192 and 32768 tokens (bf16, and int8 with the
+    fp16 scales of the reference's KVCache)."""
     import torch
 
     dev = torch.device("cuda:0")
@@ -502,6 +503,15 @@ def bench_small_config(pkg, steps: int, warmup: int):
         tf = flops / (t["mean_ms"] * 1e-3) / 1e12
         out[f"prefill_B1_T{T}"] = {**_timing_fields(t), "TFLOPs_back_to_back": round(tf, 1),
                                    "frac_of_bf16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
+    # float16 prefill (V read in place by transposed LDS reads, no V repack launch)
+    for T in (512, 2048):
+        q = (torch.randn(1, Hq, T, D, device=dev, generator=g) * 0.5).to(torch.float16)
+        k = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.float16)
+        v = (torch.randn(1, Hkv, T, D, device=dev, generator=g) * 0.5).to(torch.float16)
+        t = time_calls(lambda: pkg.attention_flash_triton(q, k, v, causal=True), steps, warmup)
+        tf = _syn().prefill_flops(1, Hq, T, D) / (t["mean_ms"] * 1e-3) / 1e12
+        out[f"prefill_f16_B1_T{T}"] = {**_timing_fields(t), "TFLOPs_back_to_back": round(tf, 1),
+                                       "frac_of_fp16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
     q = torch.randn(1, Hq, 1, D, device=dev, generator=g).to(torch.bfloat16)
     for S in (8192, 32768):
         kv_len = torch.tensor([S], dtype=torch.int32, device=dev)
@@ -522,7 +532,8 @@ def bench_small_config(pkg, steps: int, warmup: int):
         out[f"decode_int8_B1_ctx{S}"] = {**_timing_fields(t), "GBps_back_to_back": round(gbs, 1),
                                          "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
     out["workload"] = ("one sequence, 32/8 heads, head_dim 128, bf16: causal prefill at the reference "
-                       "benchmark's lengths; decode over a contiguous cache (rates from back-to-back calls)")
+                       "benchmark's lengths (and fp16 at two of them); decode over a contiguous cache "
+                       "(rates from back-to-back calls)")
     return out
 
 
