@@ -224,6 +224,24 @@ def test_f16_raw_v_rows(gpu_pkg, B, Tq, Tk, causal, token_major):
     check_every_head(out, q, k, v, causal, f"f16 raw V Tq={Tq} Tk={Tk}")
 
 
+@pytest.mark.parametrize("D", [32, 64])
+@pytest.mark.parametrize("B,Hq,Hkv,Tq,Tk,causal,token_major", [(2, 32, 8, 900, 900, True, True),
+                                                                (1, 16, 16, 333, 1001, False, True),
+                                                                (3, 8, 2, 700, 513, True, False)])
+def test_f16_raw_v_rows_small_head_dims(gpu_pkg, D, B, Hq, Hkv, Tq, Tk, causal, token_major):
+    """float16 raw V rows and transposed reads at head_dim 32 and 64 (their
+    own V-row swizzles; 16 and 8 rows per 1 KB transfer): ragged key blocks,
+    Tq != Tk, token-major storage read in place, MHA and GQA, every head
+    against the oracle."""
+    announce(f"prefill f16 raw V D={D} B={B} {Hq}/{Hkv} Tq={Tq} Tk={Tk} causal={causal}")
+    q, k, v = qkv(B, Hq, Hkv, Tq, Tk, D, torch.float16, seed=D + Tq + Tk)
+    if token_major:
+        q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
+    out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
+    torch.cuda.synchronize()
+    check_every_head(out, q, k, v, causal, f"f16 raw V D={D} Tq={Tq} Tk={Tk}")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("Tq,Tk,causal,token_major", [(256, 256, True, False), (257, 257, True, True),
                                                        (40, 256, True, True), (256, 256, False, True),
