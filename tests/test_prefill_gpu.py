@@ -265,7 +265,7 @@ def test_short_key_ranges(gpu_pkg, dtype, Tq, Tk, causal, token_major):
 
 
 @pytest.mark.parametrize("D", [64, 128])
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_empty_lengths(gpu_pkg, D, dtype):
     """No keys: every row sees nothing and is written as zeros, the
     reference's guard of a fully masked row (kernels/attention_kernel.py:224-226).
