@@ -149,6 +149,13 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   if (Tk > 1 && (k_sn < 2 * D || k_sn * kPfBN >= ((int64_t)1 << 31)))
     return fail(SIA_ERR_UNSUPPORTED, "k token stride %lld bytes: expected [%lld, 2^31/64)", (long long)k_sn,
                 (long long)(2 * D));
+  // float16 V at head_dim 32-128 is read in place like K (no V^T images)
+  const bool v_in_place = q->dtype == SIA_F16 && D >= 32 && D <= 128;
+  const int64_t v_sn = bstride(v, 2);
+  const bool v_rows_ok = Tk <= 1 || (v_sn >= 2 * D && v_sn * kPfBN < ((int64_t)1 << 31));
+  if (v_in_place && !v_rows_ok)
+    return fail(SIA_ERR_UNSUPPORTED, "v token stride %lld bytes: expected [%lld, 2^31/64)", (long long)v_sn,
+                (long long)(2 * D));
   if (!(sm_scale > 0.f) || !isfinite(sm_scale)) return fail(SIA_ERR_INVALID_ARGUMENT, "sm_scale must be positive");
   if (q->dtype == SIA_F32) {
     if (rope != nullptr)
@@ -217,14 +224,9 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   // every work-group builds the V^T images of its key blocks in LDS
   // (variant 2) instead of prefill_pack_v building them, one launch less.
   // The raw V rows take the K rows' path (32-bit offsets within a block).
-  const int64_t v_sn = p.v_sn;
-  const bool v_rows_ok = Tk <= 1 || (v_sn >= 2 * D && v_sn * kPfBN < ((int64_t)1 << 31));
-  if (q->dtype == SIA_F16 && D >= 32 && D <= 128) {
+  if (v_in_place) {
     // float16 V needs no conversion: every variant takes raw V rows and reads
     // them transposed from LDS (no V^T images, no repack)
-    if (!v_rows_ok)
-      return fail(SIA_ERR_UNSUPPORTED, "v token stride %lld bytes: expected [%lld, 2^31/64)", (long long)v_sn,
-                  (long long)(2 * D));
     a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
     p.nblocks = 0;
   } else if (L.var == 1 && rope == nullptr && Tk <= kPackvMaxKeys && (int64_t)a.nqblk * nunit <= dev.cus &&

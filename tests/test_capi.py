@@ -74,6 +74,33 @@ def test_null_arguments_are_rejected_without_launching(lib):
     assert rc == -1
 
 
+def test_prefill_f16_v_rows_checked_on_the_host(lib):
+    """float16 V at head_dim 128 is read in place, so its token stride is
+    checked like K's, on the host, before any device query: rows closer than
+    one row's bytes are refused (SIA_ERR_UNSUPPORTED).  The same descriptors in
+    bfloat16 pass that check (V is repacked) and stop at the missing workspace."""
+    from importlib import import_module
+    lm = import_module("simple-inference-autoresearch_amd._lib")
+
+    def d(dtype, shape, stride, addr):
+        t = lm.SiaTensor()
+        t.data, t.dtype, t.ndim = addr, dtype, 4
+        for i in range(4):
+            t.shape[i], t.stride[i] = shape[i], stride[i]
+        return t
+
+    for dtype, want in ((0, -2), (1, -3)):   # SIA_F16: unsupported; SIA_BF16: workspace
+        q = d(dtype, (1, 8, 4, 128), (4096, 512, 128, 1), 0x10000)
+        k = d(dtype, (1, 2, 4, 128), (1024, 512, 128, 1), 0x20000)
+        v = d(dtype, (1, 2, 4, 128), (1024, 512, 64, 1), 0x30000)    # rows 128 bytes apart, 256 long
+        o = d(dtype, (1, 8, 4, 128), (4096, 512, 128, 1), 0x40000)
+        rc = lib.sia_attention_flash_fwd(ctypes.byref(q), ctypes.byref(k), ctypes.byref(v), 1, ctypes.c_float(0.1),
+                                         ctypes.byref(o), None, 0, None)
+        assert rc == want, (dtype, rc, lib.sia_last_error_message())
+        if dtype == 0:
+            assert b"v token stride" in lib.sia_last_error_message()
+
+
 def test_no_cpu_fallback(monkeypatch):
     """Without the HIP library (or without a GPU) the product path raises."""
     pkg = load_pkg()
