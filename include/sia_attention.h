@@ -177,8 +177,8 @@ int sia_paged_gqa_int8_flash_decode_noalloc(const sia_tensor* q, const sia_tenso
  * (else SIA_ERR_UNSUPPORTED).
  * workspace: device memory of at least sia_prefill_workspace_size bytes
  * (256-byte aligned); it holds V converted to f16 in the kernel's block
- * layout (float16 V at head_dim 32-128 needs none of it) and is free again
- * when the stream passes the call.  f32 inputs run in fp32 on the vector
+ * layout (float16 V at head_dim 32-128 needs none: NULL, 0 is accepted
+ * there) and is free again when the stream passes the call.  f32 inputs run in fp32 on the vector
  * ALUs and need no workspace (NULL, 0 is accepted). */
 int sia_attention_flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int32_t causal,
                             float sm_scale, const sia_tensor* out, void* workspace, size_t workspace_bytes,

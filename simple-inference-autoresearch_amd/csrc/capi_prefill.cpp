@@ -162,7 +162,7 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
       return fail(SIA_ERR_UNSUPPORTED, "the rotary prologue runs on the float16/bfloat16 MFMA path only");
     return prefill_f32(q, k, v, causal, sm_scale, out, stream);
   }
-  const int64_t need = image_bytes(B, Hkv, Tk, D);
+  const int64_t need = v_in_place ? 0 : image_bytes(B, Hkv, Tk, D);   // (V^T images)
   if (need > 0 && (workspace == nullptr || (uintptr_t)workspace % 256 || workspace_bytes < (size_t)need))
     return fail(SIA_ERR_WORKSPACE, "prefill workspace missing, misaligned or smaller than %lld bytes",
                 (long long)need);

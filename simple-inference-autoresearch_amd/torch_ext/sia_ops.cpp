@@ -188,6 +188,14 @@ Tensor readable(const Tensor& t) {
   return ok ? t : t.contiguous();
 }
 
+// The prefill takes no workspace for fp32 (vector-ALU path) and for float16
+// at head_dim 32-128, whose V is read in place; otherwise V is repacked into
+// f16 block images in the workspace.
+bool v_in_place(const Tensor& q) {
+  const int64_t D = q.size(-1);
+  return q.scalar_type() == at::kFloat || (q.scalar_type() == at::kHalf && D >= 32 && D <= 128);
+}
+
 // Causal / full attention (q (B, Hq, Tq, D)) -> (B, Hq, Tq, D) or token-major (B, Tq, Hq, D).
 Tensor prefill(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, bool causal, double sm_scale,
                bool out_token_major) {
@@ -202,10 +210,10 @@ Tensor prefill(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, bool 
   const Tensor view = out_token_major ? out.transpose(1, 2) : out;
   const sia_tensor dout = desc(view, dev, "out");
   size_t ws_bytes = 0;
-  if (q.scalar_type() != at::kFloat) check(sia_prefill_workspace_size(B, Hkv, Tk, D, &ws_bytes));
-  Tensor ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
-  check(sia_attention_flash_fwd(&dq, &dk, &dv, causal ? 1 : 0, (float)sm_scale, &dout, ws.data_ptr(), ws_bytes,
-                                stream_of(dev)));
+  if (!v_in_place(q)) check(sia_prefill_workspace_size(B, Hkv, Tk, D, &ws_bytes));
+  Tensor ws = ws_bytes > 0 ? at::empty({(int64_t)ws_bytes}, q.options().dtype(at::kByte)) : Tensor();
+  check(sia_attention_flash_fwd(&dq, &dk, &dv, causal ? 1 : 0, (float)sm_scale, &dout,
+                                ws_bytes > 0 ? ws.data_ptr() : nullptr, ws_bytes, stream_of(dev)));
   return out;
 }
 
@@ -226,10 +234,11 @@ Tensor prefill_rope(const Tensor& q_in, const Tensor& k_in, const Tensor& v_in, 
   const Tensor view = out_token_major ? out.transpose(1, 2) : out;
   const sia_tensor dout = desc(view, dev, "out");
   size_t ws_bytes = 0;
-  if (q.scalar_type() != at::kFloat) check(sia_prefill_workspace_size(B, Hkv, Tk, D, &ws_bytes));
-  Tensor ws = at::empty({(int64_t)(ws_bytes > 0 ? ws_bytes : 1)}, q.options().dtype(at::kByte));
+  if (!v_in_place(q)) check(sia_prefill_workspace_size(B, Hkv, Tk, D, &ws_bytes));
+  Tensor ws = ws_bytes > 0 ? at::empty({(int64_t)ws_bytes}, q.options().dtype(at::kByte)) : Tensor();
   check(sia_attention_flash_fwd_rope(&dq, &dk, &dv, &dc, &dsn, interleaved ? 1 : 0, dsp.ptr(), (int32_t)start_offset,
-                                     causal ? 1 : 0, (float)sm_scale, &dout, ws.data_ptr(), ws_bytes,
+                                     causal ? 1 : 0, (float)sm_scale, &dout, ws_bytes > 0 ? ws.data_ptr() : nullptr,
+                                     ws_bytes,
                                      stream_of(dev)));
   return out;
 }

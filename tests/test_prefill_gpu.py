@@ -224,6 +224,33 @@ def test_f16_raw_v_rows(gpu_pkg, B, Tq, Tk, causal, token_major):
     check_every_head(out, q, k, v, causal, f"f16 raw V Tq={Tq} Tk={Tk}")
 
 
+@pytest.mark.parametrize("D", [32, 128])
+def test_f16_needs_no_workspace(gpu_pkg, D):
+    """Through the C ABI: float16 V read in place takes no workspace (NULL, 0),
+    and gives the bits of the extension's call; bfloat16 still asks for one."""
+    import ctypes
+    from importlib import import_module
+    lm = import_module("simple-inference-autoresearch_amd._lib")
+    lib = lm.load_library()
+    announce(f"prefill f16 without workspace D={D}")
+    q, k, v = qkv(2, 16, 4, 300, 300, D, torch.float16, seed=D + 5)
+    ref = gpu_pkg.attention_flash_triton(q, k, v, causal=True)
+    out = torch.full_like(ref, float("nan"))
+    dq, dk, dv, do = (lm.desc(t) for t in (q, k, v, out))
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.sia_attention_flash_fwd(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv), 1,
+                                     ctypes.c_float(1.0 / (D ** 0.5)), ctypes.byref(do), None, 0, stream)
+    torch.cuda.synchronize()
+    assert rc == 0, lib.sia_last_error_message()
+    assert torch.equal(out, ref)
+    qb, kb, vb = (t.to(torch.bfloat16) for t in (q, k, v))
+    ob = torch.empty_like(qb)
+    dq, dk, dv, do = (lm.desc(t) for t in (qb, kb, vb, ob))
+    rc = lib.sia_attention_flash_fwd(ctypes.byref(dq), ctypes.byref(dk), ctypes.byref(dv), 1,
+                                     ctypes.c_float(1.0 / (D ** 0.5)), ctypes.byref(do), None, 0, stream)
+    assert rc == -3   # SIA_ERR_WORKSPACE: bfloat16 V is repacked into the workspace
+
+
 @pytest.mark.parametrize("D", [32, 64])
 @pytest.mark.parametrize("B,Hq,Hkv,Tq,Tk,causal,token_major", [(2, 32, 8, 900, 900, True, True),
                                                                 (1, 16, 16, 333, 1001, False, True),
