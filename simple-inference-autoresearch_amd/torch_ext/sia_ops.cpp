@@ -190,7 +190,9 @@ Tensor readable(const Tensor& t) {
 
 // The prefill takes no workspace for fp32 (vector-ALU path) and for float16
 // at head_dim 32-128, whose V is read in place; otherwise V is repacked into
-// f16 block images in the workspace.
+// f16 block images in the workspace.  (The same rule as v_in_place in
+// csrc/capi_prefill.cpp; were they to differ, the library would refuse the
+// call with SIA_ERR_WORKSPACE rather than touch memory it was not given.)
 bool v_in_place(const Tensor& q) {
   const int64_t D = q.size(-1);
   return q.scalar_type() == at::kFloat || (q.scalar_type() == at::kHalf && D >= 32 && D <= 128);
