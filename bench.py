@@ -249,7 +249,21 @@ def bench_prefill_config(pkg, steps: int, warmup: int):
             "statistic": (f"TFLOPs: the {steps} timed calls issued back to back between two synchronizes (as the "
                           f"headline's value); TFLOPs_median_call: median of a separate pass of {steps} calls "
                           "with an event between calls"),
-            "rope_prologue": bench_rope_prologue(pkg, q, k, v, steps, warmup)}
+            "rope_prologue": bench_rope_prologue(pkg, q, k, v, steps, warmup),
+            "fp16_same_shape": bench_prefill_f16(pkg, q, k, v, steps, warmup)}
+
+
+def bench_prefill_f16(pkg, q, k, v, steps: int, warmup: int):
+    """The config-4 shape in float16, whose V the kernel reads in place (no V repack
+    launch); same 2.5 PFLOP/s dense peak."""
+    import torch
+
+    qh, kh, vh = (t.to(torch.float16) for t in (q, k, v))
+    B, Hq, T, D = q.shape
+    t = time_calls(lambda: pkg.attention_flash_triton(qh, kh, vh, causal=True, out_token_major=True), steps, warmup)
+    tf = _syn().prefill_flops(B, Hq, T, D) / (t["mean_ms"] * 1e-3) / 1e12
+    return {"us_per_call": round(t["median_ms"] * 1e3, 2), "us_per_call_back_to_back": round(t["mean_ms"] * 1e3, 2),
+            "TFLOPs": round(tf, 1), "frac_of_fp16_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4)}
 
 
 def bench_rope_prologue(pkg, q, k, v, steps: int, warmup: int):
