@@ -98,9 +98,10 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 //    and a two-stage ring, so twice the work-groups, and a causal work-group
 //    covers half the rows (B1 T = 1024: 30.5 -> 25.6 us per call).
 //    Variant 2 is variant 1 without prefill_pack_v: V blocks come into the
-//    ring as raw rows and every work-group builds the f16 V^T image of each
-//    block in LDS (more vector work per block, one launch less per call;
-//    chosen for short key ranges, where the call is launch- and latency-bound).
+//    ring as raw rows, every work-group converts each bfloat16 block to f16
+//    in LDS, and the PV product reads it with transposed reads (more vector
+//    work per block, one launch less per call; chosen for short key ranges,
+//    where the call is launch- and latency-bound).
 //    float16 at D = 32 ... 128 needs no V^T images in any variant: raw V rows
 //    and transposed LDS reads (kTrV in prefill_fwd).
 //  * D <= 64: 4 waves with the same register budget, so two work-groups share
@@ -401,8 +402,8 @@ void prefill_fwd(const PrefillArgs a) {
   // 2e-3 output bar.  D = 16 keeps the images, zero-padded to the 32-wide PV
   // tile.  D = 256, one wave per SIMD, lost 11% to the two reads per operand
   // against the repack's one launch.)
-  constexpr bool kTrV = std::is_same<T, F16>::value && D >= 32 && D <= 128;
-  constexpr bool kRawV = C::packv || kTrV;      // raw V rows in the V stages
+  constexpr bool kTrV = (std::is_same<T, F16>::value && D >= 32 && D <= 128) || C::packv;
+  constexpr bool kRawV = kTrV;                  // raw V rows in the V stages
   // K stages: swizzled row-major (below); V^T image chunk c of dimension d at
   // c * D * 16 + d * 16
   // (distinct arrays per stage: the compiler then sees that a DMA into one
@@ -628,51 +629,38 @@ void prefill_fwd(const PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) issue_v1(blk, LV, i);
   };
-  // Variant 2: turn the raw V block of stage LV (key rows, swizzled as the K
-  // stages) into its f16 V^T image, in place.  Every thread gathers 4
-  // dimensions of one 8-key image chunk group (8 LDS reads of 8 bytes); after
-  // a barrier (every raw row read) it writes those 4 image chunks over the
-  // stage, and a second barrier makes the image whole.
+  // Variant 2 with bfloat16 V: convert the raw V block of stage LV to f16 in
+  // place (the transposed reads then take it as they take float16 V).  Every
+  // thread converts its own 16-byte chunks (bf16 bits as f32, clamped to the
+  // f16 range, both halves rounded in one packed conversion: prefill_pack_v's
+  // arithmetic), so one barrier after the writes suffices.
   auto pack_vstage = [&](char* LV) {
-    if constexpr (C::packv && !kTrV) {
-      static_assert(NK == NV && KB == VB && DV == D && NW * 64 == 8 * (D / 4), "variant 2 geometry");
+    if constexpr (C::packv && std::is_same<T, BF16>::value) {
+      constexpr int CH = VB / 16 / (NW * 64);
+      static_assert(CH * 16 * NW * 64 == VB, "variant 2 geometry");
       __builtin_amdgcn_sched_barrier(0);
       // (t passes through an empty asm so that the address arithmetic stays
       // inside this step: hoisted out of the key loop, its registers would be
       // held across every block)
       int t = threadIdx.x;
       asm volatile("" : "+v"(t));
-      const int c = t / (D / 4), d0 = 4 * (t % (D / 4));
-      u32x2 r[8];
+      u32x4 w[CH];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = image_key(c, i);
-        r[i] = *(const u32x2*)(LV + k * RB + (((d0 >> 3) ^ (k % NC)) * 16) + (d0 & 7) * 2);
-      }
-      u32x4 w[4];
+      for (int i = 0; i < CH; ++i) w[i] = *(const u32x4*)(LV + (t + i * NW * 64) * 16);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int i = 0; i < CH; ++i)
 #pragma unroll
         for (int m = 0; m < 4; ++m) {
-          const uint32_t x0 = r[2 * m][tt >> 1], x1 = r[2 * m + 1][tt >> 1];
-          if constexpr (std::is_same<T, BF16>::value) {
-            // the bf16 bits as f32 (shift or mask), clamped to the f16 range,
-            // both rounded in one packed conversion: elem_f16's result
-            const float f0 = __builtin_bit_cast(float, (tt & 1) ? (x0 & 0xffff0000u) : (x0 << 16));
-            const float f1 = __builtin_bit_cast(float, (tt & 1) ? (x1 & 0xffff0000u) : (x1 << 16));
-            w[tt][m] = pack2(F16{}, __builtin_amdgcn_fmed3f(f0, -65504.0f, 65504.0f),
-                             __builtin_amdgcn_fmed3f(f1, -65504.0f, 65504.0f));
-          } else {
-            const uint32_t e0 = (x0 >> (16 * (tt & 1))) & 0xffffu, e1 = (x1 >> (16 * (tt & 1))) & 0xffffu;
-            w[tt][m] = e0 | (e1 << 16);
-          }
+          const uint32_t x = w[i][m];
+          const float f0 = __builtin_bit_cast(float, x << 16), f1 = __builtin_bit_cast(float, x & 0xffff0000u);
+          w[i][m] = pack2(F16{}, __builtin_amdgcn_fmed3f(f0, -65504.0f, 65504.0f),
+                          __builtin_amdgcn_fmed3f(f1, -65504.0f, 65504.0f));
         }
-      ring_barrier();     // every raw row of the stage is read
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) *(u32x4*)(LV + (c * DV + d0 + tt) * 16) = w[tt];
-      ring_barrier();     // the whole image is written before any wave reads it
+      for (int i = 0; i < CH; ++i) *(u32x4*)(LV + (t + i * NW * 64) * 16) = w[i];
+      ring_barrier();     // the whole converted block is written before any wave reads it
       // (nothing of the block step that follows is scheduled into the
-      // conversion, where its registers would add to the pack's)
+      // conversion, where its registers would add to it)
       __builtin_amdgcn_sched_barrier(0);
     }
   };

@@ -16,11 +16,14 @@ struct PrefillLaunch {
 };
 
 // Longest key range that runs variant 2 (bfloat16: float16 at D = 128 reads
-// raw V rows at every length and never repacks).  The in-LDS conversion costs a
-// work-group ~0.65 us per 64-key block, the separate repack ~3 us per call
-// (its launch and one load/store round trip): one sequence of 128 tokens
-// 9.8 -> 8.1 us per call, but 512 tokens 15.7 -> 18.1 and 1024 24.0 -> 31.0.
-constexpr int kPackvMaxKeys = 256;
+// raw V rows at every length and never repacks).  Converting each block in
+// LDS costs the work-group ~0.1 us per 64-key block (its 16 KB read,
+// converted and written back, one barrier); the separate repack ~3 us per
+// call plus a kernel boundary.  One sequence at 32/8 heads, per call back to
+// back: 128 / 256 / 384 / 512 tokens 8.15 / 11.24 / 13.89 / 15.84 ->
+// 7.45 / 9.97 / 12.48 / 15.16 us, but 768 tokens 19.97 -> 20.24 and 1024
+// 24.07 -> 25.32.
+constexpr int kPackvMaxKeys = 512;
 
 int launch_prefill(PrefillLaunch& L);
 

@@ -270,14 +270,15 @@ def test_f16_raw_v_rows_small_head_dims(gpu_pkg, D, B, Hq, Hkv, Tq, Tk, causal, 
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("Tq,Tk,causal,token_major", [(256, 256, True, False), (257, 257, True, True),
+@pytest.mark.parametrize("Tq,Tk,causal,token_major", [(256, 256, True, False), (512, 512, True, True),
+                                                       (513, 513, True, True),
                                                        (40, 256, True, True), (256, 256, False, True),
                                                        (200, 255, False, False), (300, 64, True, False)])
 def test_short_key_ranges(gpu_pkg, dtype, Tq, Tk, causal, token_major):
-    """head_dim 128 with at most 256 keys on a small grid: with bfloat16 each
-    work-group builds the f16 V^T images of its key blocks in LDS from raw V
-    rows (no separate repack launch); 257 keys and up take the repack (float16
-    reads raw V rows at every length).  Both sides of
+    """head_dim 128 with at most 512 keys on a small grid: with bfloat16 each
+    work-group converts its raw V blocks to f16 in LDS and reads them with
+    transposed reads (no separate repack launch); 513 keys and up take the
+    repack (float16 reads raw V rows at every length).  Both sides of
     the cut-over, chunked rows (Tq < Tk), Tq > Tk, and K/V read in place
     from token-major (B, T, H, D) storage, every head against the oracle."""
     announce(f"prefill short key range {dtype} Tq={Tq} Tk={Tk} causal={causal} token_major={token_major}")
