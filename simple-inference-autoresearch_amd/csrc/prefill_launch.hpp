@@ -17,7 +17,7 @@ struct PrefillLaunch {
 
 // Longest key range that runs variant 2 (bfloat16: float16 at D = 128 reads
 // raw V rows at every length and never repacks).  Converting each block in
-// LDS costs the work-group ~0.1 us per 64-key block (its 16 KB read,
+// LDS costs the work-group ~0.3 us per 64-key block (its 16 KB read,
 // converted and written back, one barrier); the separate repack ~3 us per
 // call plus a kernel boundary.  One sequence at 32/8 heads, per call back to
 // back: 128 / 256 / 384 / 512 tokens 8.15 / 11.24 / 13.89 / 15.84 ->
