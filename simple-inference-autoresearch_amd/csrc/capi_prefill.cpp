@@ -221,16 +221,15 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   p.Hkv = (int)Hkv; p.Tk = (int)Tk; p.nkb = a.nkb;
   p.nblocks = B * Hkv * a.nkb;
   // Short key ranges on the 4-wave variant whose grid fits the CUs once:
-  // every work-group builds the V^T images of its key blocks in LDS
-  // (variant 2) instead of prefill_pack_v building them, one launch less.
+  // every work-group converts the bf16 V blocks it walks to f16 in LDS
+  // (variant 2) instead of prefill_pack_v repacking V, one launch less.
   // The raw V rows take the K rows' path (32-bit offsets within a block).
   if (v_in_place) {
     // float16 V needs no conversion: every variant takes raw V rows and reads
     // them transposed from LDS (no V^T images, no repack)
     a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
     p.nblocks = 0;
-  } else if (L.var == 1 && rope == nullptr && Tk <= kPackvMaxKeys && (int64_t)a.nqblk * nunit <= dev.cus &&
-             v_rows_ok) {
+  } else if (L.var == 1 && Tk <= kPackvMaxKeys && (int64_t)a.nqblk * nunit <= dev.cus && v_rows_ok) {
     L.var = 2;
     a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
     p.nblocks = 0;   // no separate repack

@@ -17,13 +17,10 @@ static int launch_prefill_typed(PrefillLaunch& L) {
     hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)L.pack.nblocks), dim3(256), 0, L.stream, L.pack);
   }
   if constexpr (D == 128) {
-    if (L.var == 2) {   // (no rotary prologue on this variant)
-      hipLaunchKernelGGL((prefill_fwd<D, T, kRopeNone, 2>), dim3(L.a.nqblk * L.a.nunit), dim3(PfCfg<D, 2>::waves * 64),
-                         0, L.stream, L.a);
-      const hipError_t e = hipGetLastError();
-      if (e != hipSuccess) return fail(SIA_ERR_LAUNCH, "prefill launch: %s", hipGetErrorString(e));
-      return SIA_OK;
-    }
+    // (variant 2 converts bf16 V in LDS; float16 V needs no conversion and
+    // runs variant 1 without a repack)
+    if constexpr (std::is_same<T, BF16>::value)
+      if (L.var == 2) return launch_fwd<D, T, 2>(L, rope);
     if (L.var == 1) return launch_fwd<D, T, 1>(L, rope);
   }
   return launch_fwd<D, T, 0>(L, rope);
