@@ -89,7 +89,8 @@ def test_fused_equals_rope_then_attention(gpu_pkg, D, dtype, interleaved):
     check(got, oracle(q, k, v, cos, sin, [9] * B, interleaved, True), f"D={D} il={interleaved}")
 
 
-@pytest.mark.parametrize("Tq,Tk,causal", [(64, 300, True), (200, 513, True), (17, 17, False), (300, 64, False)])
+@pytest.mark.parametrize("Tq,Tk,causal", [(64, 300, True), (200, 513, True), (512, 512, True), (17, 17, False),
+                                          (300, 64, False)])
 def test_chunked_and_full(gpu_pkg, Tq, Tk, causal):
     """Chunked prefill (Tq < Tk, queries at positions Tk - Tq + i) and non-causal attention."""
     announce(f"rope prefill Tq={Tq} Tk={Tk} causal={causal}")
