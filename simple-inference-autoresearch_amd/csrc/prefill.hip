@@ -16,13 +16,12 @@ static int launch_prefill_typed(PrefillLaunch& L) {
     // one work-group per 64-key V^T image
     hipLaunchKernelGGL((prefill_pack_v<D, T>), dim3((unsigned)L.pack.nblocks), dim3(256), 0, L.stream, L.pack);
   }
-  if constexpr (D == 128) {
-    // (variant 2 converts bf16 V in LDS; float16 V needs no conversion and
-    // runs variant 1 without a repack)
-    if constexpr (std::is_same<T, BF16>::value)
-      if (L.var == 2) return launch_fwd<D, T, 2>(L, rope);
+  // (variant 2 converts bf16 V in LDS; float16 V needs no conversion and
+  // runs without a repack in any variant)
+  if constexpr ((D == 64 || D == 128) && std::is_same<T, BF16>::value)
+    if (L.var == 2) return launch_fwd<D, T, 2>(L, rope);
+  if constexpr (D == 128)
     if (L.var == 1) return launch_fwd<D, T, 1>(L, rope);
-  }
   return launch_fwd<D, T, 0>(L, rope);
 }
 

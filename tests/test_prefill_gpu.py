@@ -274,15 +274,16 @@ def test_f16_raw_v_rows_small_head_dims(gpu_pkg, D, B, Hq, Hkv, Tq, Tk, causal, 
                                                        (513, 513, True, True),
                                                        (40, 256, True, True), (256, 256, False, True),
                                                        (200, 255, False, False), (300, 64, True, False)])
-def test_short_key_ranges(gpu_pkg, dtype, Tq, Tk, causal, token_major):
-    """head_dim 128 with at most 512 keys on a small grid: with bfloat16 each
+@pytest.mark.parametrize("D", [64, 128])
+def test_short_key_ranges(gpu_pkg, D, dtype, Tq, Tk, causal, token_major):
+    """head_dim 64 and 128 with at most 512 keys on a small grid: with bfloat16 each
     work-group converts its raw V blocks to f16 in LDS and reads them with
     transposed reads (no separate repack launch); 513 keys and up take the
     repack (float16 reads raw V rows at every length).  Both sides of
     the cut-over, chunked rows (Tq < Tk), Tq > Tk, and K/V read in place
     from token-major (B, T, H, D) storage, every head against the oracle."""
-    announce(f"prefill short key range {dtype} Tq={Tq} Tk={Tk} causal={causal} token_major={token_major}")
-    q, k, v = qkv(2, 16, 4, Tq, Tk, 128, dtype, seed=Tq * 3 + Tk)
+    announce(f"prefill short key range D={D} {dtype} Tq={Tq} Tk={Tk} causal={causal} token_major={token_major}")
+    q, k, v = qkv(2, 16, 4, Tq, Tk, D, dtype, seed=Tq * 3 + Tk + D)
     if token_major:   # (B, T, H, D) storage seen as (B, H, T, D): row stride H*D elements
         q, k, v = (t.transpose(1, 2).contiguous().transpose(1, 2) for t in (q, k, v))
     out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
