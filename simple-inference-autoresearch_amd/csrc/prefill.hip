@@ -18,7 +18,7 @@ static int launch_prefill_typed(PrefillLaunch& L) {
   }
   // (variant 2 converts bf16 V in LDS; float16 V needs no conversion and
   // runs without a repack in any variant)
-  if constexpr ((D == 64 || D == 128) && std::is_same<T, BF16>::value)
+  if constexpr ((D == 32 || D == 64 || D == 128) && std::is_same<T, BF16>::value)
     if (L.var == 2) return launch_fwd<D, T, 2>(L, rope);
   if constexpr (D == 128)
     if (L.var == 1) return launch_fwd<D, T, 1>(L, rope);

@@ -97,7 +97,7 @@ constexpr int kBufferFlags = 0x00020000;   // gfx9 raw buffer resource word 3 (3
 //    exceed the CU count, e.g. one sequence of up to 2048 tokens): 4 waves
 //    and a two-stage ring, so twice the work-groups, and a causal work-group
 //    covers half the rows (B1 T = 1024: 30.5 -> 25.6 us per call).
-//    Variant 2 (D = 64 too) is variant 1 without prefill_pack_v: V blocks come into the
+//    Variant 2 (D = 32 and 64 too) is variant 1 without prefill_pack_v: V blocks come into the
 //    ring as raw rows, every work-group converts each bfloat16 block to f16
 //    in LDS, and the PV product reads it with transposed reads (more vector
 //    work per block, one launch less per call; chosen for short key ranges,

@@ -274,9 +274,9 @@ def test_f16_raw_v_rows_small_head_dims(gpu_pkg, D, B, Hq, Hkv, Tq, Tk, causal, 
                                                        (513, 513, True, True),
                                                        (40, 256, True, True), (256, 256, False, True),
                                                        (200, 255, False, False), (300, 64, True, False)])
-@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("D", [32, 64, 128])
 def test_short_key_ranges(gpu_pkg, D, dtype, Tq, Tk, causal, token_major):
-    """head_dim 64 and 128 with at most 512 keys on a small grid: with bfloat16 each
+    """head_dim 32, 64 and 128 with at most 512 keys on a small grid: with bfloat16 each
     work-group converts its raw V blocks to f16 in LDS and reads them with
     transposed reads (no separate repack launch); 513 keys and up take the
     repack (float16 reads raw V rows at every length).  Both sides of
