@@ -220,7 +220,7 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
   p.vimg = (char*)workspace;
   p.Hkv = (int)Hkv; p.Tk = (int)Tk; p.nkb = a.nkb;
   p.nblocks = B * Hkv * a.nkb;
-  // Short key ranges on the 4-wave variant whose grid fits the CUs once:
+  // Short key ranges on a 4-wave grid of at most two work-groups per CU:
   // every work-group converts the bf16 V blocks it walks to f16 in LDS
   // (variant 2) instead of prefill_pack_v repacking V, one launch less.
   // The raw V rows take the K rows' path (32-bit offsets within a block).
@@ -229,7 +229,8 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
     // them transposed from LDS (no V^T images, no repack)
     a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
     p.nblocks = 0;
-  } else if ((L.var == 1 || ((D == 32 || D == 64) && L.var == 0)) && Tk <= kPackvMaxKeys && (int64_t)a.nqblk * nunit <= dev.cus &&
+  } else if ((L.var == 1 || ((D == 32 || D == 64) && L.var == 0)) && Tk <= kPackvMaxKeys &&
+             (int64_t)a.nqblk * nunit <= 2 * (int64_t)dev.cus &&
              v_rows_ok) {
     L.var = 2;
     a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
