@@ -24,6 +24,10 @@ struct PrefillLaunch {
 // 7.45 / 9.97 / 12.48 / 15.16 us, but 768 tokens 19.97 -> 20.24 and 1024
 // 24.07 -> 25.32.
 constexpr int kPackvMaxKeys = 512;
+// The same at D = 32 and 64, whose blocks (4 and 8 KB) cost less to convert:
+// 768 tokens 13.41 -> 12.78 us (D = 32) and 17.41 -> 16.76 (D = 64), 1024
+// tokens 16.15 -> 16.24 and 20.81 -> 20.98.
+constexpr int kPackvMaxKeysD64 = 768;
 
 int launch_prefill(PrefillLaunch& L);
 

@@ -224,10 +224,12 @@ def test_f16_raw_v_rows(gpu_pkg, B, Tq, Tk, causal, token_major):
     check_every_head(out, q, k, v, causal, f"f16 raw V Tq={Tq} Tk={Tk}")
 
 
-@pytest.mark.parametrize("D,B,T,causal", [(128, 8, 256, True), (64, 4, 512, True), (32, 4, 512, False)])
+@pytest.mark.parametrize("D,B,T,causal", [(128, 8, 256, True), (64, 4, 512, True), (32, 4, 512, False),
+                                           (64, 1, 768, True), (32, 1, 769, True)])
 def test_short_keys_two_groups_per_cu(gpu_pkg, D, B, T, causal):
     """bf16 variant 2 (V converted in LDS, no repack) on a grid of about two
-    work-groups per CU (32/8 heads): every head against the oracle."""
+    work-groups per CU (32/8 heads), and at D <= 64 on both sides of its
+    768-key cut-over: every head against the oracle."""
     announce(f"prefill short keys, large grid D={D} B={B} T={T} causal={causal}")
     q, k, v = qkv(B, 32, 8, T, T, D, torch.bfloat16, seed=D + B + T)
     out = gpu_pkg.attention_flash_triton(q, k, v, causal=causal)
