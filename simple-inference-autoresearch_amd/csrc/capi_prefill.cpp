@@ -229,7 +229,8 @@ int flash_fwd(const sia_tensor* q, const sia_tensor* k, const sia_tensor* v, int
     // them transposed from LDS (no V^T images, no repack)
     a.v = p.v; a.v_sb = p.v_sb; a.v_sh = p.v_sh; a.v_sn = v_sn;
     p.nblocks = 0;
-  } else if ((L.var == 1 || ((D == 32 || D == 64) && L.var == 0)) && Tk <= (D <= 64 ? kPackvMaxKeysD64 : kPackvMaxKeys) &&
+  } else if (q->dtype == SIA_BF16 && (L.var == 1 || ((D == 32 || D == 64) && L.var == 0)) &&
+             Tk <= (D <= 64 ? kPackvMaxKeysD64 : kPackvMaxKeys) &&
              (int64_t)a.nqblk * nunit <= 2 * (int64_t)dev.cus &&
              v_rows_ok) {
     L.var = 2;
