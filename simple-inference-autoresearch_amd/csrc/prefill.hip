@@ -22,6 +22,9 @@ static int launch_prefill_typed(PrefillLaunch& L) {
     if (L.var == 2) return launch_fwd<D, T, 2>(L, rope);
   if constexpr (D == 128)
     if (L.var == 1) return launch_fwd<D, T, 1>(L, rope);
+  // (a variant the host picked but this head_dim/dtype has no kernel for
+  // would run the images path on V^T images nobody wrote)
+  if (L.var != 0) return fail(SIA_ERR_LAUNCH, "prefill variant %d is not built for head_dim %d", L.var, D);
   return launch_fwd<D, T, 0>(L, rope);
 }
 
